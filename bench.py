@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X backend on BASELINE.json's headline configurations.
+
+Headline (``value``): config C2, the bf16 NT GEMM at M=N=K=4096 with fp32
+accumulation, in TFLOP/s; a "step" is one GEMM launch over inputs already
+resident in HBM.  The int8 weight-only decode GEMV (config C3, GB/s against
+the HBM roofline) and the other configs are reported under ``secondary``.
+
+Timing: ``--warmup`` untimed launches, then ``--steps`` launches bracketed by
+torch.cuda.synchronize() and HIP events recorded on the stream the kernels
+are launched on (torch's current stream, which the C ABI is handed).
+
+The GEMV's weights (45 MB) would fit in the 256 MB MALL, so its timed loop
+rotates over enough weight copies (> 256 MB) that every launch streams its
+weights from HBM.
+
+``cpu_baseline`` times the oracle (the C restatement of momijo's CPU tensor
+engine, single-threaded as the reference is) on a row slab of C2, on this
+box's host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def _args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5)")
+    return p.parse_args()
+
+
+def _time_launches(fn, steps: int, warmup: int):
+    """Average ms per launch of fn() over `steps` launches (HIP events on the
+    current stream), after `warmup` untimed ones."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _rand_bf16(shape, seed, std=1.0):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(shape, generator=g, device="cuda") * std).to(torch.bfloat16)
+
+
+def _rand_f32(shape, seed, std=1.0):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(shape, generator=g, device="cuda") * std
+
+
+def bench_c2(steps, warmup):
+    import momijo_amd as mj
+    M = N = K = 4096
+    A = _rand_bf16((M, K), 1)
+    B = _rand_bf16((N, K), 2)
+    C = mj.gemm_bf16_nt(A, B)
+    ms = _time_launches(lambda i: mj.gemm_bf16_nt(A, B, out=C), steps, warmup)
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "name": "c2_bf16_gemm_4096",
+        "metric": "bf16 NT GEMM TFLOP/s at 4096^3",
+        "value": tflops, "unit": "TFLOP/s", "ms_per_launch": ms,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": None},
+        "flops_per_launch": flops,
+    }
+
+
+def bench_c3(steps, warmup):
+    import torch
+    import momijo_amd as mj
+    N, K = 11008, 4096
+    W = _rand_f32((N, K), 4, 0.02)
+    q0, s = mj.quantize_rowwise_int8(W)
+    del W
+    bias = (torch.rand(N, device="cuda") - 0.5) / 8
+    x = _rand_bf16((1, K), 3)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    copies = 8  # 8 x 45 MB > the 256 MB MALL: each launch reads from HBM
+    qs = [q0] + [q0.clone() for _ in range(copies - 1)]
+    lins = [mj.W8Linear(q, s, bias) for q in qs]
+    n_launch = max(steps, 400)
+    ms = _time_launches(lambda i: lins[i % copies].forward(x, out=y), n_launch, max(warmup, 16))
+    hot_ms = _time_launches(lambda i: lins[0].forward(x, out=y), n_launch, max(warmup, 16))
+    bytes_ = N * K + N * 4 + K * 2 + N * 4 + N * 2   # Q + scales + x + bias(f32) + y
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    return {
+        "name": "c3_int8_gemv_11008x4096",
+        "metric": "int8 weight-only GEMV GB/s (M=1)",
+        "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+        "bytes_per_launch": bytes_,
+        "weights_rotated_over": copies,
+        "cache_hot_GBs": bytes_ / (hot_ms * 1e-3) / 1e9,
+    }
+
+
+def bench_c3_pack(steps, warmup):
+    import torch
+    import momijo_amd as mj
+    from momijo_amd import _lib
+    N, K = 11008, 4096
+    Ws = [_rand_f32((N, K), 4 + i, 0.02) for i in range(2)]  # 2 x 180 MB: no MALL reuse
+    q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    s = torch.empty((N,), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(i):
+        _lib.call("mj_quantize_rowwise_i8", Ws[i % 2].data_ptr(), N, K, _lib.ROUND_RHE,
+                  q.data_ptr(), s.data_ptr(), stream)
+
+    ms = _time_launches(run, max(steps // 2, 20), warmup)
+    bytes_ = N * K * 4 + N * K + N * 4
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    return {
+        "name": "c3pack_quantize_rowwise_11008x4096",
+        "metric": "per-channel int8 quantize/pack GB/s",
+        "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+        "bytes_per_launch": bytes_,
+    }
+
+
+def bench_c4(steps, warmup):
+    import torch
+    import momijo_amd as mj
+    M, N, K = 2048, 4096, 4096
+    lin = mj.W8Linear.from_float(_rand_f32((N, K), 6, 0.02),
+                                 (torch.rand(N, device="cuda") - 0.5) / 8, mj.EPI_GELU_TANH)
+    x = _rand_bf16((M, K), 5)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ms = _time_launches(lambda i: lin.forward(x, out=y), steps, warmup)
+    flops = 2.0 * M * N * K
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "name": "c4_w8a16_prefill_gelu_2048x4096x4096",
+        "metric": "W8A16 GEMM + bias + GELU TFLOP/s",
+        "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+    }
+
+
+def bench_c5(steps, warmup):
+    import torch
+    import momijo_amd as mj
+    M, K, I, H = 512, 4096, 11008, 4096
+    g = mj.W8Linear.from_float(_rand_f32((I, K), 6, 0.02))
+    u = mj.W8Linear.from_float(_rand_f32((I, K), 7, 0.02))
+    d = mj.W8Linear.from_float(_rand_f32((H, I), 8, 0.02))
+    mlp = mj.W8MLP(g, u, d)
+    x = _rand_bf16((M, K), 9)
+    h = torch.empty((M, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    ms = _time_launches(lambda i: mlp.forward(x, h, y), steps, warmup)
+    flops = 3 * 2.0 * M * K * I
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "name": "c5_w8a16_mlp_512x4096x11008",
+        "metric": "W8A16 Llama FFN TFLOP/s (gate/up + down)",
+        "value": tf, "unit": "TFLOP/s", "ms_per_step": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+    }
+
+
+def bench_c1(steps, warmup):
+    import torch
+    import momijo_amd as mj
+    x = mj.Tensor(_rand_f32((256, 256), 1))
+    lin = mj.Linear(256, 256)
+    lin.weight.torch.copy_(_rand_f32((256, 256), 2))
+    lin.bias_t.torch.copy_((torch.rand(256, device="cuda") - 0.5) / 8)
+    ms = _time_launches(lambda i: lin.forward_act(x, mj.EPI_RELU), steps, warmup)
+    flops = 2.0 * 256 ** 3
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "name": "c1_fp32_linear_relu_256",
+        "metric": "fp32 Linear(256->256)+bias+ReLU TFLOP/s",
+        "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_FP32_TFLOPS, "traffic": None},
+    }
+
+
+def cpu_baseline_c2(rows: int = 128):
+    """The oracle's strict-k fp32 dot on upcast bf16 inputs (momijo's CPU
+    engine applied to bf16 data, single thread) over `rows` rows of C2."""
+    import numpy as np
+    import oracle
+    oracle.build()
+    K = N = 4096
+    A = oracle.f32_to_bf16(oracle.randn_f32((rows, K), seed=1))
+    B = oracle.f32_to_bf16(oracle.randn_f32((N, K), seed=2))
+    t0 = time.perf_counter()
+    oracle.gemm_bf16_nt(A, B, rows=(0, rows))
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * N * K
+    del np
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"C2 row slab: {rows} of 4096 rows x N=4096 x K=4096 "
+                      f"({dt:.1f} s, oracle/momijo_oracle.c mo_gemm_bf16_nt, gcc -O2, 1 thread)",
+            "host_nproc": os.cpu_count()}
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": f"--gpus {a.gpus}: this backend is single-GPU; every GPU box "
+                                   "in this setup has one GPU, so only --gpus 1 is measured"}))
+        sys.exit(2)
+    import torch
+    import momijo_amd as mj
+    if not mj.gpu_available():
+        print(json.dumps({"error": "no gfx950 device or libmomijo_hip.so not built"}))
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    only = set(filter(None, a.only.split(",")))
+    want = lambda k: not only or k in only  # noqa: E731
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    head = bench_c2(a.steps, a.warmup) if want("c2") else None
+    print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
+    secondary = []
+    for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
+                    ("c5", bench_c5), ("c1", bench_c1)):
+        if want(key):
+            r = fn(a.steps, a.warmup)
+            secondary.append(r)
+            print(f"# {key} done: {r['value']:.1f} {r['unit']}", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    gpu_wall = time.perf_counter() - t0
+
+    cpu = None
+    if not a.no_cpu and want("c2"):
+        cpu = cpu_baseline_c2()
+        print(f"# cpu baseline done: {cpu['value']:.2e} TFLOP/s", file=sys.stderr, flush=True)
+
+    out = {
+        "metric": "GEMM TFLOP/s (% MFMA peak) at 4096^3 bf16; int8 GEMV GB/s (% HBM peak)",
+        "value": head["value"] if head else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": head["ms_per_launch"] if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.randn on device, seeded)",
+        "config": {"workload": "C2: bf16 NT GEMM M=N=K=4096, fp32 accumulate, bf16 out",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "roofline": head["roofline"] if head else None,
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+        "gpu_wall_s": gpu_wall,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,193 @@
+/*
+ * momijo_hip.h -- C ABI of the MI355X (gfx950) backend for momijo's
+ * tensor-engine hot path: dense matmul / Linear, the int8 weight path and the
+ * bias + activation epilogue.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, returns
+ * an int32 status (MJ_OK = 0) and never throws.  Unless a name ends in `_h`,
+ * pointers are DEVICE pointers (HIP global memory of the current device) and
+ * the call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ * stream).  `_h` variants take HOST pointers, copy in, run and copy out
+ * synchronously, which is the ownership model of the reference's own device
+ * seam (tensor/gpu/runtime.mojo:539-631).
+ *
+ * Layout conventions: row-major with explicit leading dimensions / strides in
+ * ELEMENTS.  bf16 values travel as uint16_t bit patterns.  Weights follow the
+ * reference's Linear layout [out_features, in_features] (learn/nn/layers.mojo:
+ * 347-348), so y = x W^T is an "NT" product.
+ *
+ * Reference citations are relative to /root/reference/legacy/src/momijo/.
+ */
+#ifndef MOMIJO_HIP_H
+#define MOMIJO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------- */
+#define MJ_OK 0
+#define MJ_ERR_ARG 1         /* null pointer, bad enum, negative size       */
+#define MJ_ERR_SHAPE 2       /* operand shapes disagree                     */
+#define MJ_ERR_UNSUPPORTED 3 /* alignment / divisibility the kernels need   */
+#define MJ_ERR_DEVICE 4      /* a HIP runtime error (launch, copy, sync)    */
+#define MJ_ERR_NO_DEVICE 5   /* no gfx950 device is visible                 */
+#define MJ_ERR_ALLOC 6       /* device allocation failed                    */
+
+/* ---- epilogues: applied to the fp32 result after scale and bias ----- */
+#define MJ_EPI_NONE 0
+#define MJ_EPI_RELU 1              /* ReLU.forward: v > 0 ? v : 0 (layers.mojo:117-137)      */
+#define MJ_EPI_GELU_TANH 2         /* gelu32 (tensor/math.mojo:288-295), finite past x~10.06 */
+#define MJ_EPI_SILU 3              /* silu32 (tensor/math.mojo:283-285)                      */
+#define MJ_EPI_GELU_TANH_APPROX 4  /* learn.nn gelu via _exp_approx (activations.mojo:158-163) */
+#define MJ_EPI_SILU_APPROX 5       /* learn.nn silu via _exp_approx (activations.mojo:137-152) */
+#define MJ_EPI_RELU_UNARY 6        /* Tensor.relu, apply_unary op 8 (tensor/math.mojo:582-585) */
+
+/* ---- int8 rounding rules -------------------------------------------- */
+#define MJ_ROUND_RHE 0     /* round half to even, clamp [-127,127] (per-channel spec)   */
+#define MJ_ROUND_LEGACY 1  /* fp32 v +- 0.5 then truncate, clamp [-128,127]
+                              (functional.mojo:208-217)                                 */
+
+/* ---- runtime ---------------------------------------------------------- */
+
+/* ABI version (major*100 + minor). */
+int32_t mj_version(void);
+
+/* 1 if a gfx950 device is usable, else 0.  Replaces gpu_available()
+ * (tensor/gpu/runtime.mojo:29-36), which is a compile-time probe there. */
+int32_t mj_device_available(void);
+
+/* Message for the last non-OK status returned on this host thread. */
+const char *mj_last_error(void);
+
+/* Waits for all work queued on `stream`. */
+int32_t mj_stream_synchronize(void *stream);
+
+/* ---- fp32 engine ------------------------------------------------------ */
+
+/* C[M,N] = epi(A @ B + bias) for fp32 operands given as (pointer, row stride,
+ * column stride), so transposed views (stride swaps, tensor/transform.mojo:
+ * 1248-1294, 2107-2136) need no copy.  bias may be NULL; C has leading
+ * dimension ldc.  Replaces matmul_core_mm (tensor/broadcast.mojo:1612-1673),
+ * reached from Tensor.matmul (tensor/tensor.mojo:3168-3169) and
+ * tensor.matmul (tensor/__init__.mojo:123). */
+int32_t mj_matmul_f32(int64_t M, int64_t N, int64_t K,
+                      const float *A, int64_t sAm, int64_t sAk,
+                      const float *B, int64_t sBk, int64_t sBn,
+                      const float *bias, int32_t epilogue,
+                      float *C, int64_t ldc, void *stream);
+
+/* y[M] = A[M,N] x[N] with strides.  Replaces matmul_core_vec
+ * (tensor/broadcast.mojo:1543-1608), Tensor.matmul_vec (tensor.mojo:3180). */
+int32_t mj_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
+                      const float *x, int64_t sx, float *y, void *stream);
+
+/* y[N,OutF] = epi(x[N,InF] W^T + b), W [OutF,InF] row-major, b [OutF] or
+ * NULL.  Replaces Linear.forward / forward_auto (learn/nn/layers.mojo:
+ * 383-433, 510-516) with the activation layer that follows it fused in. */
+int32_t mj_linear_f32(const float *x, const float *W, const float *bias, int32_t epilogue,
+                      float *y, int64_t N, int64_t InF, int64_t OutF, void *stream);
+
+/* Host-pointer seam with the signature of launch_1d_linear_fw
+ * (tensor/gpu/runtime.mojo:539-631): x [N,InF], wT [InF,OutF] (the layout
+ * Linear.forward_gpu builds, layers.mojo:489-497), b [OutF], y [N,OutF];
+ * y[n,o] = sum_k x[n,k] wT[k,o] + b[o] as the seam's CPU kernel
+ * _kernel_linear_fw (layers.mojo:436-475) defines it.  Synchronous. */
+int32_t mj_launch_linear_fw_h(const float *x, const float *wT, const float *b, float *y,
+                              int64_t N, int64_t InF, int64_t OutF, int32_t has_bias);
+
+/* Elementwise fp32 activation y = epi(x) over n elements (may alias).
+ * Replaces Tensor.relu / silu / gelu (tensor/tensor.mojo:3848,4003,4020 ->
+ * apply_unary, tensor/math.mojo:566-638) and ReLU.forward (layers.mojo:134). */
+int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream);
+
+/* ---- bf16 -------------------------------------------------------------- */
+
+/* C[M,N] = bf16(epi(A[M,K] B[N,K]^T + bias)), fp32 accumulation on bf16
+ * MFMA.  No reference counterpart: momijo has no bf16 matmul (broadcast.mojo
+ * has f64/f32 overloads only, :1531,1677); its result is defined as the fp32
+ * engine on exactly upcast bf16 inputs.  Needs K % 8 == 0, lda/ldb/ldc % 8
+ * == 0 and 16-byte aligned A, B, C. */
+int32_t mj_gemm_bf16_nt(int64_t M, int64_t N, int64_t K,
+                        const uint16_t *A, int64_t lda, const uint16_t *B, int64_t ldb,
+                        const float *bias, int32_t epilogue,
+                        uint16_t *C, int64_t ldc, void *stream);
+
+/* ---- int8: legacy per-tensor W8A8 (QuantLinear) ------------------------- */
+
+/* q[i] = clamp(round(x[i]/scale)) with the MJ_ROUND_LEGACY rule; scale 0 is
+ * replaced by 1.  Replaces quantize_symmetric_int8 (learn/api/functional.mojo:
+ * 231-247). */
+int32_t mj_quantize_symmetric_int8(const float *x, int64_t n, float scale, int8_t *q, void *stream);
+
+/* minmax_out (device fp32 [2]) = {min x, max x} over n > 0 elements: the
+ * reduction of MinMaxObserver.observe (learn/api/sequential.mojo:232-250). */
+int32_t mj_minmax_f32(const float *x, int64_t n, float *minmax_out, void *stream);
+
+/* *scale_out (device fp32) = max(|min x|, |max x|) / max_q, or 1.0 when n == 0,
+ * max_q <= 0 or the magnitude is 0.  Replaces MinMaxObserver.observe +
+ * scale_symmetric (learn/api/sequential.mojo:232-263). */
+int32_t mj_minmax_scale_symmetric(const float *x, int64_t n, float max_q, float *scale_out,
+                                  void *stream);
+
+/* C[M,N] int32 = A[M,K] int8 * B^T, B = w_q [N,K] int8, exact int32
+ * accumulation on int8 MFMA.  legacy_literal = 1 instead reads B as
+ * reshape(w_q.flat, [K,N]) exactly as matmul_i8_i8_to_i32 does when handed
+ * the stride view w_q.transpose() (learn/api/functional.mojo:249-279, :274).
+ * K % 16 == 0 with 16-byte aligned A and B runs on int8 MFMA; other shapes
+ * take a scalar kernel with the same (exact) result. */
+int32_t mj_matmul_i8_i8_to_i32(const int8_t *A, const int8_t *B, int32_t *C,
+                               int64_t M, int64_t N, int64_t K, int32_t legacy_literal,
+                               void *stream);
+
+/* y[M,N] = float(acc) * sf + b[N] (rounded multiply, then rounded add).
+ * Replaces dequantize_i32_to_f32_add_bias (learn/api/functional.mojo:281-302). */
+int32_t mj_dequantize_i32_to_f32_add_bias(const int32_t *acc, float sf, const float *b, float *y,
+                                          int64_t M, int64_t N, void *stream);
+
+/* QuantLinear.forward (learn/nn/layers.mojo:1681-1685): quantize x [M,K]
+ * with s_x, int8 GEMM against w_q [N,K], y = float(acc)*(s_x*s_w) + b.
+ * The dequantize is fused into the GEMM epilogue; the int8 copy of x lives in
+ * a device workspace the library owns. */
+int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b,
+                            float s_w, float s_x, float *y,
+                            int64_t M, int64_t N, int64_t K, int32_t legacy_literal,
+                            void *stream);
+
+/* ---- int8: per-output-channel weight-only (BASELINE spec) -------------- */
+
+/* Q[N,K] int8 and scales[N] from W[N,K] fp32, one scale per output row.
+ * MJ_ROUND_RHE: scale = max|row|/127 (1.0 for an all-zero row),
+ *               q = clamp(rne(w/scale), -127, 127).
+ * MJ_ROUND_LEGACY: scale = MinMax rule per row (sequential.mojo:252-263),
+ *               q by functional.mojo:214-217.
+ * The per-tensor reference path is quantize_symmetric_int8 + convert
+ * (sequential.mojo:436-450); this is its per-row generalisation. */
+int32_t mj_quantize_rowwise_i8(const float *W, int64_t N, int64_t K, int32_t rounding,
+                               int8_t *Q, float *scales, void *stream);
+
+/* y[M,N] = bf16(epi((x[M,K] . Q[N,K]^T) * scales[N] + bias[N])) with x bf16,
+ * fp32 accumulation.  M <= 8 runs the streaming GEMV kernel, larger M the
+ * MFMA GEMM with int8 -> bf16 conversion on the way into LDS.  bias may be
+ * NULL.  Needs K % 16 == 0 and 16-byte aligned x, Q, y. */
+int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
+                        const float *bias, int32_t epilogue, uint16_t *y,
+                        int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Llama-style FFN on W8A16 weights (composition of Linear, silu32 and the
+ * elementwise product, tensor/tensor.mojo:4373):
+ *   h[M,I] = bf16(silu32(x Wg^T * sg) * (x Wu^T * su))   (one fused GEMM)
+ *   y[M,H] = bf16((h Wd^T) * sd)
+ * Wg, Wu [I,K]; Wd [H,I]; h is a caller-owned [M,I] buffer. */
+int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
+                     const int8_t *Wu, const float *su, const int8_t *Wd, const float *sd,
+                     uint16_t *h, uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H,
+                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOMIJO_HIP_H */

@@ -1,0 +1,306 @@
+// C ABI of the backend (declared in include/momijo_hip.h).  Each entry point
+// validates its arguments, picks a kernel configuration and enqueues on the
+// caller's stream; nothing here throws, every failure is a status code plus a
+// per-thread message from mj_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/momijo_hip.h"
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int32_t hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return MJ_OK;
+  return fail(MJ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool valid_epi(int32_t e) { return e >= MJ_EPI_NONE && e <= MJ_EPI_RELU_UNARY; }
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+int32_t check_dims(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) return fail(MJ_ERR_ARG, "negative size (M=%lld N=%lld K=%lld)",
+                                           (long long)M, (long long)N, (long long)K);
+  if (M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(MJ_ERR_UNSUPPORTED, "dimension exceeds 2^31");
+  return MJ_OK;
+}
+
+hipStream_t S(void *stream) { return (hipStream_t)stream; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t mj_version(void) { return 100; }
+
+int32_t mj_device_available(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+const char *mj_last_error(void) { return g_err; }
+
+int32_t mj_stream_synchronize(void *stream) {
+  return hip_status(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+}
+
+// ------------------------------------------------------------------ fp32
+int32_t mj_matmul_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm, int64_t sAk,
+                      const float *B, int64_t sBk, int64_t sBn, const float *bias,
+                      int32_t epilogue, float *C, int64_t ldc, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
+  if (ldc < N) return fail(MJ_ERR_SHAPE, "ldc (%lld) < N (%lld)", (long long)ldc, (long long)N);
+  if (sAm < 0 || sAk < 0 || sBk < 0 || sBn < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+  return hip_status(mj::launch_gemm_f32(M, N, K, A, sAm, sAk, B, sBk, sBn, bias, epilogue, C,
+                                        ldc, S(stream)),
+                    "gemm_f32 launch");
+}
+
+int32_t mj_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
+                      const float *x, int64_t sx, float *y, void *stream) {
+  if (int32_t s = check_dims(M, N, 0)) return s;
+  if (M == 0) return MJ_OK;
+  if (!y || (N > 0 && (!A || !x))) return fail(MJ_ERR_ARG, "null operand");
+  if (sAm < 0 || sAn < 0 || sx < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+  return hip_status(mj::launch_matvec_f32(M, N, A, sAm, sAn, x, sx, y, S(stream)),
+                    "matvec_f32 launch");
+}
+
+int32_t mj_linear_f32(const float *x, const float *W, const float *bias, int32_t epilogue,
+                      float *y, int64_t N, int64_t InF, int64_t OutF, void *stream) {
+  // y = x W^T: B = W^T is the stride view (sBk = 1, sBn = InF) of W.
+  return mj_matmul_f32(N, OutF, InF, x, InF, 1, W, 1, InF, bias, epilogue, y, OutF, stream);
+}
+
+int32_t mj_launch_linear_fw_h(const float *x, const float *wT, const float *b, float *y,
+                              int64_t N, int64_t InF, int64_t OutF, int32_t has_bias) {
+  if (int32_t s = check_dims(N, OutF, InF)) return s;
+  if (N == 0 || OutF == 0) return MJ_OK;
+  if (!y || (InF > 0 && (!x || !wT)) || (has_bias && !b)) return fail(MJ_ERR_ARG, "null operand");
+  const size_t bx = (size_t)N * InF * 4, bw = (size_t)InF * OutF * 4, by = (size_t)N * OutF * 4,
+               bb = (size_t)OutF * 4;
+  char *dev = nullptr;
+  const size_t total = bx + bw + by + bb + 64;
+  if (hipMalloc((void **)&dev, total) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "hipMalloc(%zu) failed", total);
+  }
+  float *dx = (float *)dev, *dw = (float *)(dev + bx), *dy = (float *)(dev + bx + bw),
+        *db = (float *)(dev + bx + bw + by);
+  int32_t st = MJ_OK;
+  if (bx) st = hip_status(hipMemcpy(dx, x, bx, hipMemcpyHostToDevice), "copy x");
+  if (!st && bw) st = hip_status(hipMemcpy(dw, wT, bw, hipMemcpyHostToDevice), "copy wT");
+  if (!st && has_bias) st = hip_status(hipMemcpy(db, b, bb, hipMemcpyHostToDevice), "copy b");
+  if (!st)
+    st = hip_status(mj::launch_gemm_f32(N, OutF, InF, dx, InF, 1, dw, OutF, 1,
+                                        has_bias ? db : nullptr, MJ_EPI_NONE, dy, OutF, nullptr),
+                    "gemm_f32 launch");
+  if (!st) st = hip_status(hipMemcpy(y, dy, by, hipMemcpyDeviceToHost), "copy y");
+  (void)hipFree(dev);
+  return st;
+}
+
+int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream) {
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (n < 0) return fail(MJ_ERR_ARG, "negative size");
+  if (n == 0) return MJ_OK;
+  if (!x || !y) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_activation_f32(epilogue, x, y, n, S(stream)), "activation launch");
+}
+
+// ------------------------------------------------------------------ bf16
+int32_t mj_gemm_bf16_nt(int64_t M, int64_t N, int64_t K, const uint16_t *A, int64_t lda,
+                        const uint16_t *B, int64_t ldb, const float *bias, int32_t epilogue,
+                        uint16_t *C, int64_t ldc, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
+  if (lda < K || ldb < K || ldc < N) return fail(MJ_ERR_SHAPE, "leading dimension too small");
+  if (K % 8 || lda % 8 || ldb % 8 || !aligned16(A) || !aligned16(B))
+    return fail(MJ_ERR_UNSUPPORTED, "bf16 GEMM needs K, lda, ldb %% 8 == 0 and 16-byte aligned A, B");
+  mj::GemmNT p;
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.bias = bias; p.epi = epilogue;
+  p.C = C; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.bkind = mj::B_BF16;
+  return hip_status(mj::launch_gemm_nt(p, S(stream)), "gemm_bf16 launch");
+}
+
+// ------------------------------------------------------------------ int8 legacy
+int32_t mj_quantize_symmetric_int8(const float *x, int64_t n, float scale, int8_t *q,
+                                   void *stream) {
+  if (n < 0) return fail(MJ_ERR_ARG, "negative size");
+  if (n == 0) return MJ_OK;
+  if (!x || !q) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_quantize_tensor_legacy(x, n, scale, q, S(stream)),
+                    "quantize launch");
+}
+
+int32_t mj_minmax_f32(const float *x, int64_t n, float *minmax_out, void *stream) {
+  if (n <= 0) return fail(MJ_ERR_ARG, "minmax needs n > 0");
+  if (!x || !minmax_out) return fail(MJ_ERR_ARG, "null operand");
+  float *part = nullptr;
+  const size_t bytes = sizeof(float) * 2 * mj::minmax_partials();
+  if (hipMallocAsync((void **)&part, bytes, S(stream)) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
+  }
+  int32_t st = hip_status(mj::launch_minmax(x, n, part, minmax_out, S(stream)), "minmax launch");
+  (void)hipFreeAsync(part, S(stream));
+  return st;
+}
+
+int32_t mj_minmax_scale_symmetric(const float *x, int64_t n, float max_q, float *scale_out,
+                                  void *stream) {
+  if (n < 0) return fail(MJ_ERR_ARG, "negative size");
+  if (!scale_out || (n > 0 && !x)) return fail(MJ_ERR_ARG, "null operand");
+  float *part = nullptr;
+  const size_t bytes = sizeof(float) * 2 * mj::minmax_partials();
+  if (hipMallocAsync((void **)&part, bytes, S(stream)) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
+  }
+  int32_t st = hip_status(mj::launch_minmax_scale(x, n, max_q, part, scale_out, S(stream)),
+                          "minmax launch");
+  (void)hipFreeAsync(part, S(stream));
+  return st;
+}
+
+int32_t mj_matmul_i8_i8_to_i32(const int8_t *A, const int8_t *B, int32_t *C, int64_t M,
+                               int64_t N, int64_t K, int32_t legacy_literal, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
+  if (legacy_literal || K % 16 || !aligned16(A) || !aligned16(B))
+    return hip_status(mj::launch_gemm_i8_scalar(A, B, C, nullptr, 0.f, nullptr, M, N, K,
+                                                legacy_literal != 0, S(stream)),
+                      "gemm_i8 scalar launch");
+  return hip_status(mj::launch_gemm_i8(A, B, C, nullptr, 0.f, nullptr, M, N, K, S(stream)),
+                    "gemm_i8 launch");
+}
+
+int32_t mj_dequantize_i32_to_f32_add_bias(const int32_t *acc, float sf, const float *b, float *y,
+                                          int64_t M, int64_t N, void *stream) {
+  if (int32_t s = check_dims(M, N, 0)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!acc || !b || !y) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_dequant_i32_bias(acc, sf, b, y, M, N, S(stream)),
+                    "dequant launch");
+}
+
+int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, float s_w,
+                            float s_x, float *y, int64_t M, int64_t N, int64_t K,
+                            int32_t legacy_literal, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
+  const bool fast = !legacy_literal && K % 16 == 0 && aligned16(Wq);  // xq is allocated aligned
+  int8_t *xq = nullptr;
+  const size_t bytes = (size_t)M * K + 16;
+  if (hipMallocAsync((void **)&xq, bytes, S(stream)) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
+  }
+  int32_t st = MJ_OK;
+  if (M * K > 0)
+    st = hip_status(mj::launch_quantize_tensor_legacy(x, M * K, s_x, xq, S(stream)),
+                    "quantize launch");
+  // sf = s_x * s_w with the reference's (unguarded) s_x (layers.mojo:1684)
+  const float sf = s_x * s_w;
+  if (!st) {
+    if (fast)
+      st = hip_status(mj::launch_gemm_i8(xq, Wq, nullptr, y, sf, b, M, N, K, S(stream)),
+                      "gemm_i8 launch");
+    else
+      st = hip_status(mj::launch_gemm_i8_scalar(xq, Wq, nullptr, y, sf, b, M, N, K,
+                                                legacy_literal != 0, S(stream)),
+                      "gemm_i8 scalar launch");
+  }
+  (void)hipFreeAsync(xq, S(stream));
+  return st;
+}
+
+// ------------------------------------------------------------------ int8 per-channel
+int32_t mj_quantize_rowwise_i8(const float *W, int64_t N, int64_t K, int32_t rounding, int8_t *Q,
+                               float *scales, void *stream) {
+  if (int32_t s = check_dims(N, 0, K)) return s;
+  if (rounding != MJ_ROUND_RHE && rounding != MJ_ROUND_LEGACY)
+    return fail(MJ_ERR_ARG, "unknown rounding %d", rounding);
+  if (N == 0) return MJ_OK;
+  if (K == 0) return fail(MJ_ERR_SHAPE, "K must be positive");
+  if (!W || !Q || !scales) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_quantize_rowwise(W, N, K, rounding, Q, scales, S(stream)),
+                    "quantize_rowwise launch");
+}
+
+int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
+                        const float *bias, int32_t epilogue, uint16_t *y, int64_t M, int64_t N,
+                        int64_t K, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!y || !scales || (K > 0 && (!x || !Q))) return fail(MJ_ERR_ARG, "null operand");
+  if (K % 16 || !aligned16(x) || !aligned16(Q))
+    return fail(MJ_ERR_UNSUPPORTED, "W8A16 Linear needs K %% 16 == 0 and 16-byte aligned x, Q");
+  if (M <= 8)
+    return hip_status(mj::launch_gemv_w8a16(x, Q, scales, bias, epilogue, y, M, N, K, S(stream)),
+                      "gemv_w8a16 launch");
+  mj::GemmNT p;
+  p.A = x; p.lda = K; p.B = Q; p.ldb = K; p.scales = scales; p.bias = bias; p.epi = epilogue;
+  p.C = y; p.ldc = N; p.M = M; p.N = N; p.K = K; p.bkind = mj::B_INT8;
+  return hip_status(mj::launch_gemm_nt(p, S(stream)), "gemm_w8a16 launch");
+}
+
+int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const int8_t *Wu,
+                     const float *su, const int8_t *Wd, const float *sd, uint16_t *h,
+                     uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H, void *stream) {
+  if (int32_t s = check_dims(M, I, K)) return s;
+  if (int32_t s = check_dims(M, H, I)) return s;
+  if (M == 0 || H == 0) return MJ_OK;
+  if (!x || !Wg || !sg || !Wu || !su || !Wd || !sd || !h || !y)
+    return fail(MJ_ERR_ARG, "null operand");
+  if (K % 16 || I % 16 || !aligned16(x) || !aligned16(Wg) || !aligned16(Wu) || !aligned16(Wd) ||
+      !aligned16(h))
+    return fail(MJ_ERR_UNSUPPORTED, "MLP needs K, I %% 16 == 0 and 16-byte aligned operands");
+  mj::GemmNT gu;
+  gu.A = x; gu.lda = K; gu.B = Wg; gu.B2 = Wu; gu.ldb = K; gu.scales = sg; gu.scales2 = su;
+  gu.C = h; gu.ldc = I; gu.M = M; gu.N = I; gu.K = K; gu.bkind = mj::B_INT8; gu.gate_up = true;
+  if (int32_t st = hip_status(mj::launch_gemm_nt(gu, S(stream)), "gate/up launch")) return st;
+  if (M <= 8)
+    return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
+                                            S(stream)),
+                      "down gemv launch");
+  mj::GemmNT dn;
+  dn.A = h; dn.lda = I; dn.B = Wd; dn.ldb = I; dn.scales = sd; dn.C = y; dn.ldc = H;
+  dn.M = M; dn.N = H; dn.K = I; dn.bkind = mj::B_INT8;
+  return hip_status(mj::launch_gemm_nt(dn, S(stream)), "down launch");
+}
+
+}  // extern "C"

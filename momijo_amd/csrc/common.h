@@ -1,0 +1,169 @@
+// Shared device helpers for the gfx950 kernels: vector types, bf16
+// conversion, the activation epilogues and small launch utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mj {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+// 16-byte streaming load (nontemporal: the data is read once).
+__device__ __forceinline__ uint4 load_nt16(const void *p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ float4 load_nt16f(const void *p) {
+  const f32x4 v = __builtin_nontemporal_load((const f32x4 *)p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Every epilogue function below disables FMA contraction so that its
+// rounding sequence is the reference's (one rounding per operation).
+// Epilogue ids; identical values to MJ_EPI_* in include/momijo_hip.h.
+enum Epi : int {
+  EPI_NONE = 0,
+  EPI_RELU = 1,
+  EPI_GELU_TANH = 2,
+  EPI_SILU = 3,
+  EPI_GELU_TANH_APPROX = 4,
+  EPI_SILU_APPROX = 5,
+  EPI_RELU_UNARY = 6,
+};
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN becomes a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------- activations
+// Tensor-engine family (tensor/math.mojo:272-295): exp is the accurate expf.
+__device__ __forceinline__ float sigmoid32(float x) {
+#pragma clang fp contract(off)
+  return 1.0f / (1.0f + expf(-x));
+}
+
+__device__ __forceinline__ float silu32(float x) {
+#pragma clang fp contract(off)
+  return x * sigmoid32(x);
+}
+
+// gelu32 with its literal tanh (e^{2t}-1)/(e^{2t}+1); where e^{2t} overflows
+// (the reference returns NaN there) the limit tanh = 1 is used.
+__device__ __forceinline__ float gelu32(float x) {
+#pragma clang fp contract(off)
+  const float k = 0.7978845608028654f, c = 0.044715f;
+  float x3 = x * x * x;
+  float t = k * (x + c * x3);
+  float e2x = expf(2.0f * t);
+  float th = __builtin_isinf(e2x) ? 1.0f : (e2x - 1.0f) / (e2x + 1.0f);
+  return 0.5f * x * (1.0f + th);
+}
+
+// learn.nn.activations family (learn/nn/activations.mojo:34-51,137-163).
+__device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
+  if (v < lo) v = lo;
+  if (v > hi) v = hi;
+  return v;
+}
+
+__device__ __forceinline__ float exp_approx32(float x) {
+#pragma clang fp contract(off)
+  float xv = clamp_ref(x, -20.0f, 20.0f);
+  float y = 1.0f + xv / 64.0f;
+  y = y * y; y = y * y; y = y * y; y = y * y; y = y * y; y = y * y;
+  return y;
+}
+
+__device__ __forceinline__ float tanh_approx32(float x) {
+#pragma clang fp contract(off)
+  float xv = clamp_ref(x, -10.0f, 10.0f);
+  float e2x = exp_approx32(2.0f * xv);
+  return (e2x - 1.0f) / (e2x + 1.0f);
+}
+
+__device__ __forceinline__ float gelu_approx32(float x) {
+#pragma clang fp contract(off)
+  const float s = 0.7978845608028654f;
+  float x3 = x * x * x;
+  float inner = s * (x + 0.044715f * x3);
+  return 0.5f * x * (1.0f + tanh_approx32(inner));
+}
+
+__device__ __forceinline__ float silu_approx32(float x) {
+#pragma clang fp contract(off)
+  return x * (1.0f / (1.0f + exp_approx32(-x)));
+}
+
+__device__ __forceinline__ float apply_epi(int epi, float v) {
+  switch (epi) {
+    case EPI_RELU: return v > 0.0f ? v : 0.0f;
+    case EPI_GELU_TANH: return gelu32(v);
+    case EPI_SILU: return silu32(v);
+    case EPI_GELU_TANH_APPROX: return gelu_approx32(v);
+    case EPI_SILU_APPROX: return silu_approx32(v);
+    case EPI_RELU_UNARY: return v < 0.0f ? 0.0f : v;
+    default: return v;
+  }
+}
+
+// ---------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------- tiles
+// Maps a linear workgroup id onto a (tile_m, tile_n) pair so that the
+// workgroups the hardware places on one XCD (ids congruent mod 8) form a
+// compact block of tiles that shares A rows and B rows in that XCD's L2:
+// the ids are first regrouped per XCD, then walked GROUP_M tile rows at a
+// time, column by column.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int group_m,
+                                            int &tm, int &tn) {
+  const int total = tiles_m * tiles_n;
+  int logical = bid;
+  if ((total & 7) == 0) logical = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int per_group = group_m * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * group_m;
+  int gsize = tiles_m - first_m;
+  if (gsize > group_m) gsize = group_m;
+  const int in_g = logical - g * per_group;
+  tm = first_m + in_g % gsize;
+  tn = in_g / gsize;
+}
+
+}  // namespace mj

@@ -1,0 +1,73 @@
+// Host-side launchers shared between the kernel files and the C ABI (api.hip).
+// All sizes are validated by the caller; these only pick a configuration and
+// enqueue on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mj {
+
+// ---- gemm_nt.hip: bf16 A x (bf16 | int8) B^T on MFMA ---------------------
+enum BKind : int { B_BF16 = 0, B_INT8 = 1 };
+
+struct GemmNT {
+  const uint16_t *A = nullptr;  // [M,K] bf16, leading dim lda
+  int64_t lda = 0;
+  const void *B = nullptr;      // [N,K] bf16 or int8, leading dim ldb
+  int64_t ldb = 0;
+  const void *B2 = nullptr;     // gate/up mode: the "up" weight [N,K]
+  const float *scales = nullptr;   // per output column (int8 B) or null
+  const float *scales2 = nullptr;  // gate/up mode: scales of B2
+  const float *bias = nullptr;     // per output column or null
+  int epi = 0;
+  uint16_t *C = nullptr;        // [M,N] bf16, leading dim ldc
+  int64_t ldc = 0;
+  int64_t M = 0, N = 0, K = 0;
+  int bkind = B_BF16;
+  bool gate_up = false;         // C = silu(A B^T * s) * (A B2^T * s2)
+};
+
+hipError_t launch_gemm_nt(const GemmNT &p, hipStream_t stream);
+
+// ---- gemm_f32.hip ---------------------------------------------------------
+hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                           int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
+                           const float *bias, int epi, float *C, int64_t ldc,
+                           hipStream_t stream);
+hipError_t launch_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
+                             const float *x, int64_t sx, float *y, hipStream_t stream);
+hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,
+                                 hipStream_t stream);
+
+// ---- gemv_w8.hip: skinny-M W8A16 -----------------------------------------
+hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
+                             const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
+                             int64_t K, hipStream_t stream);
+
+// ---- quant.hip -------------------------------------------------------------
+hipError_t launch_quantize_rowwise(const float *W, int64_t N, int64_t K, int rounding,
+                                   int8_t *Q, float *scales, hipStream_t stream);
+hipError_t launch_quantize_tensor_legacy(const float *x, int64_t n, float scale, int8_t *q,
+                                         hipStream_t stream);
+// partials must hold 2 * minmax_partials() floats
+int minmax_partials();
+hipError_t launch_minmax(const float *x, int64_t n, float *partials, float *minmax_out,
+                         hipStream_t stream);
+hipError_t launch_minmax_scale(const float *x, int64_t n, float max_q, float *partials,
+                               float *scale_out, hipStream_t stream);
+hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b, float *y,
+                                   int64_t M, int64_t N, hipStream_t stream);
+
+// ---- gemm_i8.hip -----------------------------------------------------------
+// C (int32) = A int8 [M,K] x B^T, B int8 [N,K]; or, with y != null, the fused
+// dequantize y = float(acc)*sf + b.
+hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
+                          const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+// Scalar fallback: literal = the reference's stride-ignoring [K,N] read of B,
+// otherwise B [N,K] for shapes/alignments the MFMA kernel does not take.
+hipError_t launch_gemm_i8_scalar(const int8_t *A, const int8_t *B, int32_t *C, float *y,
+                                 float sf, const float *b, int64_t M, int64_t N, int64_t K,
+                                 bool literal, hipStream_t stream);
+
+}  // namespace mj

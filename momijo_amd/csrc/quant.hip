@@ -1,0 +1,264 @@
+// int8 quantize / pack and the small int8 helpers of momijo's PTQ path
+// (learn/api/functional.mojo:206-302, learn/api/sequential.mojo:217-263).
+//
+// quantize_rowwise: one wave per weight row.  For K <= 4096 (K % 256 == 0)
+// the row is read once with 16-byte loads into registers (16 KiB per row),
+// reduced to its absmax / min-max with a wave butterfly, then quantized from
+// registers and written as 4-byte words: the kernel touches every byte of W
+// and Q exactly once, so it is HBM-bound.  The division w/scale is the IEEE
+// correctly rounded one (built with -fhip-fp32-correctly-rounded-divide-sqrt)
+// so results are bit-identical to a CPU fp32 division.
+#include "common.h"
+#include "launch.h"
+
+namespace mj {
+
+enum Rounding : int { ROUND_RHE = 0, ROUND_LEGACY = 1 };
+
+// _round_to_i32 + _clamp_int8 (functional.mojo:208-217): fp32 add of +-0.5,
+// truncation toward zero, clamp to [-128, 127]; NaN -> 0.
+__device__ __forceinline__ int quant_legacy(float x, float scale) {
+#pragma clang fp contract(off)
+  const float v = x / scale;
+  const float t = v + (v >= 0.0f ? 0.5f : -0.5f);
+  if (t != t) return 0;
+  if (t >= 127.0f) return 127;
+  if (t <= -128.0f) return -128;
+  return (int)t;
+}
+
+// round half to even, clamp to [-127, 127].
+__device__ __forceinline__ int quant_rhe(float x, float scale) {
+  float v = __builtin_rintf(x / scale);
+  v = v > 127.0f ? 127.0f : v;
+  v = v < -127.0f ? -127.0f : v;
+  return (int)v;
+}
+
+__device__ __forceinline__ float row_scale(int rounding, float amax, float mn, float mx) {
+  if (rounding == ROUND_RHE) {
+    const float s = amax / 127.0f;
+    return s == 0.0f ? 1.0f : s;
+  }
+  // MinMaxObserver.scale_symmetric(127) (sequential.mojo:252-263)
+  const float a = mn < 0.0f ? -mn : mn;
+  const float b = mx < 0.0f ? -mx : mx;
+  const float m = b > a ? b : a;
+  if (m <= 0.0f) return 1.0f;
+  return m / 127.0f;
+}
+
+__device__ __forceinline__ uint32_t quant4(int rounding, float4 w, float s) {
+  int q0, q1, q2, q3;
+  if (rounding == ROUND_RHE) {
+    q0 = quant_rhe(w.x, s); q1 = quant_rhe(w.y, s); q2 = quant_rhe(w.z, s); q3 = quant_rhe(w.w, s);
+  } else {
+    q0 = quant_legacy(w.x, s); q1 = quant_legacy(w.y, s);
+    q2 = quant_legacy(w.z, s); q3 = quant_legacy(w.w, s);
+  }
+  return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+         ((uint32_t)(q3 & 0xFF) << 24);
+}
+
+// Register path: K == CH * 256.
+template <int CH>
+__global__ __launch_bounds__(256) void quantize_rowwise_reg(const float *__restrict__ W, int N,
+                                                            int K, int rounding,
+                                                            int8_t *__restrict__ Q,
+                                                            float *__restrict__ scales) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= N) return;
+  const float4 *w4 = (const float4 *)(W + (size_t)row * K);
+  float4 w[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) w[c] = load_nt16f(w4 + c * 64 + lane);
+  float amax = 0.0f, mn = w[0].x, mx = w[0].x;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(w[c].x), fabsf(w[c].y)), fmaxf(fabsf(w[c].z), fabsf(w[c].w))));
+    mn = fminf(mn, fminf(fminf(w[c].x, w[c].y), fminf(w[c].z, w[c].w)));
+    mx = fmaxf(mx, fmaxf(fmaxf(w[c].x, w[c].y), fmaxf(w[c].z, w[c].w)));
+  }
+  amax = wave_max(amax);
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const float s = row_scale(rounding, amax, mn, mx);
+  uint32_t *q4 = (uint32_t *)(Q + (size_t)row * K);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) q4[c * 64 + lane] = quant4(rounding, w[c], s);
+  if (lane == 0) scales[row] = s;
+}
+
+// Generic path: any K, two passes over the row (the second mostly from L2).
+__global__ __launch_bounds__(256) void quantize_rowwise_any(const float *__restrict__ W, int N,
+                                                            int K, int rounding,
+                                                            int8_t *__restrict__ Q,
+                                                            float *__restrict__ scales) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= N) return;
+  const float *w = W + (size_t)row * K;
+  float amax = 0.0f, mn = w[0], mx = w[0];
+  for (int k = lane; k < K; k += 64) {
+    const float v = w[k];
+    amax = fmaxf(amax, fabsf(v));
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  amax = wave_max(amax);
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const float s = row_scale(rounding, amax, mn, mx);
+  for (int k = lane; k < K; k += 64)
+    Q[(size_t)row * K + k] = (int8_t)(rounding == ROUND_RHE ? quant_rhe(w[k], s) : quant_legacy(w[k], s));
+  if (lane == 0) scales[row] = s;
+}
+
+hipError_t launch_quantize_rowwise(const float *W, int64_t N, int64_t K, int rounding,
+                                   int8_t *Q, float *scales, hipStream_t stream) {
+  const unsigned blocks = (unsigned)((N + 3) / 4);
+  const bool aligned = ((uintptr_t)W % 16 == 0) && ((uintptr_t)Q % 4 == 0);
+  if (aligned && K % 256 == 0 && K <= 4096) {
+    switch (K / 256) {
+#define MJ_Q_CASE(ch)                                                                        \
+  case ch:                                                                                   \
+    hipLaunchKernelGGL(quantize_rowwise_reg<ch>, dim3(blocks), dim3(256), 0, stream, W,       \
+                       (int)N, (int)K, rounding, Q, scales);                                   \
+    return hipGetLastError();
+      MJ_Q_CASE(1) MJ_Q_CASE(2) MJ_Q_CASE(3) MJ_Q_CASE(4) MJ_Q_CASE(5) MJ_Q_CASE(6)
+      MJ_Q_CASE(7) MJ_Q_CASE(8) MJ_Q_CASE(9) MJ_Q_CASE(10) MJ_Q_CASE(11) MJ_Q_CASE(12)
+      MJ_Q_CASE(13) MJ_Q_CASE(14) MJ_Q_CASE(15) MJ_Q_CASE(16)
+#undef MJ_Q_CASE
+      default: break;
+    }
+  }
+  hipLaunchKernelGGL(quantize_rowwise_any, dim3(blocks), dim3(256), 0, stream, W, (int)N, (int)K,
+                     rounding, Q, scales);
+  return hipGetLastError();
+}
+
+// quantize_symmetric_int8 (functional.mojo:231-247), per-tensor scale.
+__global__ __launch_bounds__(256) void quantize_tensor_legacy(const float *__restrict__ x, int64_t n,
+                                                              float scale,
+                                                              int8_t *__restrict__ q) {
+  const float s = scale == 0.0f ? 1.0f : scale;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    q[i] = (int8_t)quant_legacy(x[i], s);
+}
+
+hipError_t launch_quantize_tensor_legacy(const float *x, int64_t n, float scale, int8_t *q,
+                                         hipStream_t stream) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(quantize_tensor_legacy, dim3((unsigned)blocks), dim3(256), 0, stream, x, n,
+                     scale, q);
+  return hipGetLastError();
+}
+
+// MinMaxObserver: per-workgroup min/max partials, then one workgroup folds
+// them and applies scale_symmetric.
+constexpr int kMinMaxBlocks = 1024;
+int minmax_partials() { return kMinMaxBlocks; }
+
+__global__ __launch_bounds__(256) void minmax_partial_kernel(const float *__restrict__ x, int64_t n,
+                                                             float *__restrict__ part) {
+  __shared__ float smn[4], smx[4];
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = x[i];
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) { smn[threadIdx.x >> 6] = mn; smx[threadIdx.x >> 6] = mx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[2 * blockIdx.x] = fminf(fminf(smn[0], smn[1]), fminf(smn[2], smn[3]));
+    part[2 * blockIdx.x + 1] = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+  }
+}
+
+// Folds the partials; with max_q < 0 it writes {min, max} instead of the
+// scale.
+__global__ __launch_bounds__(64) void minmax_final_kernel(const float *__restrict__ part, int np,
+                                                          int64_t n, float max_q,
+                                                          float *__restrict__ out) {
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  for (int i = threadIdx.x; i < np; i += 64) {
+    mn = fminf(mn, part[2 * i]);
+    mx = fmaxf(mx, part[2 * i + 1]);
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  if (threadIdx.x == 0 && max_q < 0.0f) {
+    out[0] = mn;
+    out[1] = mx;
+  } else if (threadIdx.x == 0) {
+    float s = 1.0f;
+    if (n > 0 && max_q > 0.0f) {
+      const float a = mn < 0.0f ? -mn : mn;
+      const float b = mx < 0.0f ? -mx : mx;
+      const float m = b > a ? b : a;
+      s = m <= 0.0f ? 1.0f : m / max_q;
+    }
+    *out = s;
+  }
+}
+
+static hipError_t minmax_impl(const float *x, int64_t n, float max_q, float *partials,
+                              float *out, hipStream_t stream) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > kMinMaxBlocks) blocks = kMinMaxBlocks;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(minmax_partial_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, n,
+                     partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(minmax_final_kernel, dim3(1), dim3(64), 0, stream, partials, (int)blocks, n,
+                     max_q, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_minmax(const float *x, int64_t n, float *partials, float *minmax_out,
+                         hipStream_t stream) {
+  return minmax_impl(x, n, -1.0f, partials, minmax_out, stream);
+}
+
+// max_q <= 0 yields scale 1.0 (scale_symmetric's guard); it is passed as 0
+// so the final kernel does not take the {min, max} branch.
+hipError_t launch_minmax_scale(const float *x, int64_t n, float max_q, float *partials,
+                               float *scale_out, hipStream_t stream) {
+  return minmax_impl(x, n, max_q > 0.0f ? max_q : 0.0f, partials, scale_out, stream);
+}
+
+// dequantize_i32_to_f32_add_bias (functional.mojo:281-302).
+__global__ __launch_bounds__(256) void dequant_i32_bias_kernel(const int32_t *__restrict__ acc,
+                                                               float sf,
+                                                               const float *__restrict__ b,
+                                                               float *__restrict__ y, int64_t M,
+                                                               int64_t N) {
+  const int64_t total = M * N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+#pragma clang fp contract(off)
+    const float v = (float)acc[i] * sf;
+    y[i] = v + b[i % N];
+  }
+}
+
+hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b, float *y,
+                                   int64_t M, int64_t N, hipStream_t stream) {
+  int64_t blocks = (M * N + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(dequant_i32_bias_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, acc,
+                     sf, b, y, M, N);
+  return hipGetLastError();
+}
+
+}  // namespace mj

@@ -1,0 +1,166 @@
+"""Layers of momijo's learn.nn on the MI355X backend: Linear, ReLU and
+QuantLinear (learn/nn/layers.mojo), plus the per-channel int8 weight-only
+Linear and the Llama-style FFN that the backend adds for bf16 activations.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from .tensor import Tensor, _device, _ptr, _stream
+
+
+class Linear:
+    """Linear(in_features, out_features, bias) (learn/nn/layers.mojo:343-794).
+
+    ``weight`` is [OutF, InF] fp32, ``bias_t`` [OutF].  ``forward`` is the
+    forward_cpu_parallel contract (:383-433): y = x W^T + b with the bias added
+    after the dot; a non-2-D input or a width mismatch returns ``x.copy()``.
+    ``forward_act`` fuses the activation layer that follows (ReLU, GELU, SiLU).
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True):
+        self.in_features = in_features
+        self.out_features = out_features
+        self.bias = bias
+        self.weight = Tensor(torch.zeros((out_features, in_features), dtype=torch.float32))
+        self.bias_t = Tensor(torch.zeros((out_features if bias else 0,), dtype=torch.float32))
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        """All weights 0.01 / in_features, bias 0 (layers.mojo:361-377)."""
+        self.weight.torch.fill_(0.01 / self.in_features)
+        if self.bias:
+            self.bias_t.torch.zero_()
+
+    def _bias_ptr(self):
+        b = self.bias_t.torch
+        return _ptr(b) if self.bias and b.numel() == self.out_features else None
+
+    def forward_act(self, x: Tensor, epi: int) -> Tensor:
+        xt = x.torch
+        if xt.dim() != 2 or xt.shape[1] != self.in_features:
+            return x.copy()
+        xt = xt.contiguous()
+        N = xt.shape[0]
+        y = torch.empty((N, self.out_features), dtype=torch.float32, device=xt.device)
+        _lib.call("mj_linear_f32", _ptr(xt), _ptr(self.weight.torch), self._bias_ptr(), epi,
+                  _ptr(y), N, self.in_features, self.out_features, _stream())
+        return Tensor(y)
+
+    def forward(self, x: Tensor) -> Tensor:
+        """Linear.forward -> forward_auto (layers.mojo:510-516)."""
+        return self.forward_act(x, _lib.EPI_NONE)
+
+    forward_auto = forward
+    forward_gpu = forward
+
+
+class ReLU:
+    """ReLU.forward = _maximum_scalar(x, 0): v > 0 ? v : 0 (layers.mojo:117-137)."""
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.maximum_scalar(0.0)
+
+
+class QuantLinear:
+    """QuantLinear (learn/nn/layers.mojo:1663-1703): per-tensor W8A8.
+
+    forward = quantize_symmetric_int8(x, s_x) -> int8 GEMM against w_q^T ->
+    float(acc) * (s_x*s_w) + b, in one quantize launch and one int8-MFMA GEMM
+    with the dequantize fused.  ``legacy_literal=True`` reproduces the
+    reference's stride-ignoring read of w_q.transpose() (functional.mojo:274).
+    """
+
+    def __init__(self, in_features: int, out_features: int, w_q: Tensor, b_f: Tensor,
+                 s_w: float, s_x: float, legacy_literal: bool = False):
+        self.in_features = in_features
+        self.out_features = out_features
+        self.w_q = Tensor(w_q.torch.contiguous())
+        self.b_f = Tensor(b_f.torch.contiguous())
+        self.s_w = float(np.float32(s_w))
+        self.s_x = float(np.float32(s_x))
+        self.legacy_literal = legacy_literal
+
+    def forward(self, x: Tensor) -> Tensor:
+        xt = x.torch.contiguous()
+        M, K = xt.shape
+        N = self.out_features
+        y = torch.empty((M, N), dtype=torch.float32, device=xt.device)
+        _lib.call("mj_quant_linear_f32", _ptr(xt), _ptr(self.w_q.torch), _ptr(self.b_f.torch),
+                  self.s_w, self.s_x, _ptr(y), M, N, K, int(self.legacy_literal), _stream())
+        return Tensor(y)
+
+
+class W8Linear:
+    """Weight-only int8 Linear with bf16 activations (per-output-channel,
+    round-half-even scales).  No reference counterpart: it is the
+    per-channel generalisation of QuantLinear's weights, applied to the
+    reference's Linear layout [OutF, InF].
+
+    y = bf16(epi((x . q^T) * scale[n] + bias[n])); M <= 8 rows take the
+    streaming GEMV kernel, more rows the MFMA GEMM."""
+
+    def __init__(self, q: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None,
+                 epi: int = _lib.EPI_NONE):
+        self.q = q.contiguous()
+        self.scales = scales.contiguous()
+        self.bias = None if bias is None else bias.float().contiguous()
+        self.epi = epi
+        self.out_features, self.in_features = self.q.shape
+
+    @classmethod
+    def from_float(cls, W: torch.Tensor, bias: torch.Tensor | None = None,
+                   epi: int = _lib.EPI_NONE, rounding: int = _lib.ROUND_RHE) -> "W8Linear":
+        q, s = quantize_rowwise_int8(W, rounding)
+        return cls(q, s, bias, epi)
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        M, K = x.shape
+        if K != self.in_features:
+            raise ValueError(f"expected {self.in_features} input features, got {K}")
+        if out is None:
+            out = torch.empty((M, self.out_features), dtype=torch.bfloat16, device=x.device)
+        _lib.call("mj_linear_w8a16", _ptr(x), _ptr(self.q), _ptr(self.scales), _ptr(self.bias),
+                  self.epi, _ptr(out), M, self.out_features, K, _stream())
+        return out
+
+
+class W8MLP:
+    """Llama-style FFN: y = ((silu(x Wg^T) * (x Wu^T)) Wd^T) on W8A16 weights.
+    The gate and up projections run as one GEMM whose epilogue forms
+    silu(g) * u; the down projection is a second W8A16 GEMM."""
+
+    def __init__(self, gate: W8Linear, up: W8Linear, down: W8Linear):
+        assert gate.q.shape == up.q.shape and down.in_features == gate.out_features
+        self.gate, self.up, self.down = gate, up, down
+
+    def forward(self, x: torch.Tensor, h: torch.Tensor | None = None,
+                out: torch.Tensor | None = None):
+        M, K = x.shape
+        I = self.gate.out_features
+        H = self.down.out_features
+        if h is None:
+            h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
+        if out is None:
+            out = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+        _lib.call("mj_mlp_w8a16", _ptr(x), _ptr(self.gate.q), _ptr(self.gate.scales),
+                  _ptr(self.up.q), _ptr(self.up.scales), _ptr(self.down.q),
+                  _ptr(self.down.scales), _ptr(h), _ptr(out), M, K, I, H, _stream())
+        return out, h
+
+
+def quantize_rowwise_int8(W: torch.Tensor, rounding: int = _lib.ROUND_RHE):
+    """Per-output-channel symmetric int8 quantize/pack of W [N,K] fp32 on the
+    device; returns (q int8 [N,K], scales fp32 [N])."""
+    W = W.float().contiguous()
+    N, K = W.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=W.device)
+    s = torch.empty((N,), dtype=torch.float32, device=W.device)
+    _lib.call("mj_quantize_rowwise_i8", _ptr(W), N, K, rounding, _ptr(q), _ptr(s), _stream())
+    return q, s
+
+
+__all__ = ["Linear", "ReLU", "QuantLinear", "W8Linear", "W8MLP", "quantize_rowwise_int8",
+           "_device"]

@@ -1,0 +1,215 @@
+"""Host-side mirror of momijo's tensor-engine operator surface on MI355X.
+
+``Tensor`` keeps the reference's ``Tensor[T]`` contract (shape, strides,
+zero-copy transpose views; tensor/tensor.mojo:776-905) with its storage in
+HBM.  Device memory and streams come from PyTorch-ROCm (plumbing only); every
+arithmetic op goes through the C ABI of ``libmomijo_hip.so``.
+
+Error behaviour follows the reference: ``matmul`` of incompatible ranks or
+shapes returns an empty tensor (tensor/broadcast.mojo:1613-1616,1677-1684).
+Device failures raise :class:`momijo_amd._lib.MomijoHipError`: unlike the
+reference's launchers (tensor/gpu/runtime.mojo:608-631) there is no silent
+CPU fallback.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    "float32": torch.float32,
+    "bfloat16": torch.bfloat16,
+    "int8": torch.int8,
+    "int32": torch.int32,
+}
+
+
+def _device() -> torch.device:
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def gpu_available() -> bool:
+    """gpu_available() (tensor/gpu/runtime.mojo:29-36): a gfx950 device and
+    the backend library are both present."""
+    try:
+        return _lib.device_available()
+    except ImportError:
+        return False
+
+
+class Tensor:
+    """A device tensor with momijo's shape/stride semantics."""
+
+    __slots__ = ("_t",)
+
+    def __init__(self, data, shape: Sequence[int] | None = None, dtype: str | None = None):
+        if isinstance(data, Tensor):
+            t = data._t
+        elif isinstance(data, torch.Tensor):
+            t = data
+        else:
+            arr = np.asarray(data)
+            if dtype == "bfloat16":
+                t = torch.from_numpy(np.ascontiguousarray(arr, np.float32)).to(torch.bfloat16)
+            else:
+                t = torch.from_numpy(np.ascontiguousarray(arr))
+        if dtype is not None and t.dtype != _DTYPES[dtype]:
+            t = t.to(_DTYPES[dtype])
+        if shape is not None:
+            t = t.reshape(list(shape))
+        if t.device.type != "cuda":
+            t = t.to(_device())
+        self._t = t
+
+    # ---------------------------------------------------------------- info
+    @property
+    def torch(self) -> torch.Tensor:
+        return self._t
+
+    def shape(self) -> list[int]:
+        return list(self._t.shape)
+
+    def strides(self) -> list[int]:
+        return list(self._t.stride())
+
+    def numel(self) -> int:
+        return self._t.numel()
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self._t.dtype
+
+    def numpy(self) -> np.ndarray:
+        t = self._t
+        if t.dtype == torch.bfloat16:
+            t = t.float()
+        return t.detach().cpu().numpy()
+
+    def copy(self) -> "Tensor":
+        return Tensor(self._t.clone())
+
+    def contiguous(self) -> "Tensor":
+        return Tensor(self._t.contiguous())
+
+    # ---------------------------------------------------------------- views
+    def transpose(self) -> "Tensor":
+        """Swap the last two axes as a zero-copy stride view
+        (tensor/tensor.mojo:2677-2679 -> tensor/transform.mojo:2132,2107-2125)."""
+        if self._t.dim() <= 1:
+            return self.copy()
+        return Tensor(self._t.transpose(-2, -1))
+
+    # ---------------------------------------------------------------- matmul
+    def matmul(self, other: "Tensor") -> "Tensor":
+        """Tensor.matmul (tensor/tensor.mojo:3168-3169)."""
+        return matmul(self, other)
+
+    def matmul_vec(self, x: "Tensor") -> "Tensor":
+        """Tensor.matmul_vec (tensor/tensor.mojo:3180-3181)."""
+        if self._t.dim() != 2 or x._t.dim() != 1 or x._t.shape[0] != self._t.shape[1]:
+            return empty_f32()
+        return _matvec(self, x)
+
+    # ---------------------------------------------------------------- unary
+    def _unary(self, epi: int) -> "Tensor":
+        if self._t.dtype != torch.float32:
+            raise TypeError("activations are defined for Float32 tensors")
+        src = self._t.contiguous()
+        out = torch.empty_like(src)
+        _lib.call("mj_activation_f32", epi, _ptr(src), _ptr(out), src.numel(), _stream())
+        return Tensor(out)
+
+    def relu(self) -> "Tensor":
+        """Tensor.relu -> apply_unary op 8 (tensor/math.mojo:582-585)."""
+        return self._unary(_lib.EPI_RELU_UNARY)
+
+    def gelu(self) -> "Tensor":
+        """Tensor.gelu -> gelu32 (tensor/math.mojo:288-295); finite where the
+        reference's tanh32 overflows (x > ~10.06)."""
+        return self._unary(_lib.EPI_GELU_TANH)
+
+    def silu(self) -> "Tensor":
+        """Tensor.silu -> silu32 (tensor/math.mojo:283-285)."""
+        return self._unary(_lib.EPI_SILU)
+
+    def maximum_scalar(self, s: float) -> "Tensor":
+        """maximum_scalar(0.0) as used between quantized layers
+        (learn/api/sequential.mojo:423).  Only s == 0 is on this path; it is
+        evaluated as v > 0 ? v : 0, equal in value to the reference's
+        where(v >= 0, v, 0) (the two differ only in the sign of a zero)."""
+        if s != 0.0:
+            raise NotImplementedError("maximum_scalar is provided for s == 0 only")
+        return self._unary(_lib.EPI_RELU)
+
+    def __repr__(self) -> str:
+        return f"Tensor(shape={self.shape()}, dtype={self._t.dtype})"
+
+
+def empty_f32() -> Tensor:
+    """empty_f32(): the reference's result for an unsupported matmul."""
+    return Tensor(torch.empty(0, dtype=torch.float32, device=_device()))
+
+
+def _matvec(A: Tensor, x: Tensor) -> Tensor:
+    a, v = A._t, x._t
+    M, N = a.shape
+    y = torch.empty(M, dtype=torch.float32, device=a.device)
+    _lib.call("mj_matvec_f32", M, N, _ptr(a), a.stride(0), a.stride(1), _ptr(v), v.stride(0),
+              _ptr(y), _stream())
+    return Tensor(y)
+
+
+def matmul(A: Tensor, B: Tensor) -> Tensor:
+    """tensor.matmul (tensor/broadcast.mojo:1677-1684): rank 2 x 1 is a matrix-
+    vector product, 2 x 2 a matrix product, anything else an empty tensor.
+
+    Float32 operands run the fp32 engine with their strides (transposed views
+    need no copy).  bfloat16 operands run the bf16 MFMA GEMM, which takes B as
+    the transpose view of a row-major [N, K] weight (x.matmul(W.transpose()))."""
+    a, b = A._t, B._t
+    if a.dim() == 2 and b.dim() == 1:
+        if a.dtype != torch.float32 or b.shape[0] != a.shape[1]:
+            return empty_f32()
+        return _matvec(A, B)
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+        return empty_f32()
+    M, K = a.shape
+    N = b.shape[1]
+    if a.dtype == torch.float32 and b.dtype == torch.float32:
+        c = torch.empty((M, N), dtype=torch.float32, device=a.device)
+        _lib.call("mj_matmul_f32", M, N, K, _ptr(a), a.stride(0), a.stride(1), _ptr(b),
+                  b.stride(0), b.stride(1), None, _lib.EPI_NONE, _ptr(c), N, _stream())
+        return Tensor(c)
+    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16:
+        if a.stride(1) != 1 or b.stride(0) != 1:
+            raise NotImplementedError(
+                "bf16 matmul takes A row-major and B as W.transpose() of a row-major W")
+        c = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+        _lib.call("mj_gemm_bf16_nt", M, N, K, _ptr(a), a.stride(0), _ptr(b), b.stride(1), None,
+                  _lib.EPI_NONE, _ptr(c), N, _stream())
+        return Tensor(c)
+    raise TypeError(f"matmul of {a.dtype} and {b.dtype} is not supported")
+
+
+def gemm_bf16_nt(A: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None,
+                 epi: int = _lib.EPI_NONE, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = bf16(epi(A @ W^T + bias)) for bf16 device tensors A [M,K], W [N,K]."""
+    M, K = A.shape
+    N = W.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    _lib.call("mj_gemm_bf16_nt", M, N, K, _ptr(A), A.stride(0), _ptr(W), W.stride(0), _ptr(bias),
+              epi, _ptr(out), out.stride(0), _stream())
+    return out

@@ -1,0 +1,93 @@
+"""GPU parity of the bf16 NT GEMM (config C2) against the oracle.
+
+The oracle is the fp32 engine on exactly upcast bf16 inputs (momijo has no
+bf16 matmul).  Bar: max|gpu - oracle| / max|oracle| <= 2e-2 (BASELINE north
+star, bf16), checked on row slabs at the full 4096^3 size; small-integer
+inputs make every sum exact, so there the bf16 outputs must be bit-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+import momijo_amd as mj
+from _util import bf16_dev, bf16_host_bits, bf16_host_f32, normwise_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def _inputs(oracle, M, N, K, seed_a=1, seed_b=2):
+    A = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed_a))
+    B = oracle.f32_to_bf16(oracle.randn_f32((N, K), seed=seed_b))
+    return A, B
+
+
+def _rows(M):
+    r = sorted(set([0, 1, 2, 31, 32, 63, 64, 127, 128, 255, M // 2, M // 2 + 1, M - 2, M - 1]))
+    return [x for x in r if 0 <= x < M]
+
+
+def _check_rows(oracle, A, B, C_dev, rows, bias=None, epi=0):
+    got = bf16_host_f32(C_dev)
+    worst = 0.0
+    for r in rows:
+        _, ref = oracle.gemm_bf16_nt(A, B, bias, epi, rows=(r, r + 1))
+        worst = max(worst, normwise_rel(got[r:r + 1], ref))
+    assert worst <= BF16_TOL, worst
+    return worst
+
+
+def test_c2_full_4096(oracle, dev):
+    M = N = K = 4096
+    A, B = _inputs(oracle, M, N, K)
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev))
+    torch.cuda.synchronize()
+    worst = _check_rows(oracle, A, B, C, _rows(M))
+    print(f"C2 4096^3 worst normwise rel err {worst:.3e}", flush=True)
+    # every output row sum against an fp64 GEMV of the row sums of B
+    # (linearity: C @ 1 = A @ (B^T 1)), a size-independent check on all rows
+    Af = oracle.bf16_to_f32(A).astype(np.float64)
+    Bf = oracle.bf16_to_f32(B).astype(np.float64)
+    ref_rowsum = Af @ Bf.sum(axis=0)
+    got_rowsum = bf16_host_f32(C).astype(np.float64).sum(axis=1)
+    scale = np.abs(Af) @ np.abs(Bf).sum(axis=0)
+    assert np.all(np.abs(got_rowsum - ref_rowsum) <= 4e-3 * scale + 1e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (100, 200, 72), (1, 8, 8), (300, 520, 1000),
+                                   (513, 257, 4096), (2048, 4096, 256)])
+def test_bf16_shapes(oracle, dev, M, N, K):
+    A, B = _inputs(oracle, M, N, K, seed_a=M + K, seed_b=N + 3 * K)
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev))
+    _check_rows(oracle, A, B, C, _rows(M))
+
+
+def test_bf16_integer_inputs_bit_exact(oracle, dev):
+    rng = np.random.default_rng(1)
+    M, N, K = 512, 384, 1024
+    Af = rng.integers(-4, 5, size=(M, K)).astype(np.float32)
+    Bf = rng.integers(-4, 5, size=(N, K)).astype(np.float32)
+    A, B = oracle.f32_to_bf16(Af), oracle.f32_to_bf16(Bf)
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev))
+    ref, _ = oracle.gemm_bf16_nt(A, B)
+    np.testing.assert_array_equal(bf16_host_bits(C), ref)
+
+
+@pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU])
+def test_bf16_bias_epilogue(oracle, dev, epi):
+    M, N, K = 320, 384, 512
+    A, B = _inputs(oracle, M, N, K, seed_a=31, seed_b=32)
+    bias = oracle.randu_f32((N,), -1.0 / 16, 1.0 / 16, seed=5)
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev), to_dev(bias, dev), epi)
+    _check_rows(oracle, A, B, C, _rows(M), bias, epi)
+
+
+def test_bf16_matmul_through_tensor_surface(oracle, dev):
+    """x.matmul(W.transpose()) on bfloat16 Tensors dispatches to the NT GEMM."""
+    M, N, K = 128, 192, 256
+    A, B = _inputs(oracle, M, N, K, seed_a=41, seed_b=42)
+    x = mj.Tensor(bf16_dev(A, dev))
+    W = mj.Tensor(bf16_dev(B, dev))
+    C = x.matmul(W.transpose()).torch
+    _check_rows(oracle, A, B, C, _rows(M))

@@ -1,0 +1,264 @@
+"""GPU parity of the int8 path against the oracle.
+
+* quantize/pack (per-channel RHE and legacy rules, per-tensor legacy):
+  bit-exact int8 and scales;
+* int8 x int8 -> int32 GEMM (legacy W8A8): bit-exact int32, and QuantLinear
+  (fused dequantize, no FMA contraction): bit-exact fp32;
+* W8A16 GEMV (C3), prefill GEMM + GELU (C4), MLP (C5): bf16 outputs within
+  max|gpu - oracle| / max|oracle| <= 2e-2, on row slabs at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+import momijo_amd as mj
+from _util import bf16_dev, bf16_host_f32, normwise_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def _quant_dev(W, dev, rounding=mj.ROUND_RHE):
+    q, s = mj.quantize_rowwise_int8(to_dev(W, dev), rounding)
+    torch.cuda.synchronize()
+    return q, s
+
+
+# ------------------------------------------------------------- quantize/pack
+def test_c3_pack_rhe_bit_exact(oracle, dev):
+    W = oracle.randn_f32((11008, 4096), std=0.02, seed=4)
+    q, s = _quant_dev(W, dev)
+    Qr, sr = oracle.quantize_rowwise_rhe(W)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(q.cpu().numpy(), Qr)
+
+
+@pytest.mark.parametrize("N,K", [(5, 256), (3, 4096), (7, 100), (2, 8192), (9, 4352)])
+@pytest.mark.parametrize("rounding", [mj.ROUND_RHE, mj.ROUND_LEGACY])
+def test_pack_shapes_and_rules(oracle, dev, N, K, rounding):
+    W = oracle.randn_f32((N, K), std=0.5, seed=N * K)
+    W[0, :] = 0.0                       # all-zero row: scale 1, q 0
+    if N > 2:
+        W[1, :] = -np.abs(W[1, :])      # absmax from a negative value
+        W[1, K // 2] = -3.0
+        W[2, :] = np.abs(W[2, :])       # absmax appearing twice
+        W[2, 0] = W[2, K - 1] = 2.0
+    q, s = _quant_dev(W, dev, rounding)
+    ref = oracle.quantize_rowwise_rhe(W) if rounding == mj.ROUND_RHE else \
+        oracle.quantize_rowwise_legacy(W)
+    np.testing.assert_array_equal(s.cpu().numpy(), ref[1])
+    np.testing.assert_array_equal(q.cpu().numpy(), ref[0])
+
+
+def test_pack_exact_ties(oracle, dev):
+    """Values (k + 1/2) * scale with a power-of-two scale, so w/scale is exact:
+    RHE rounds ties to even, the legacy rule away from zero."""
+    K = 256
+    s = np.float32(2.0 ** -6)
+    ks = np.arange(-127, 127, dtype=np.float32)[:K - 2]
+    row = np.concatenate([(ks + 0.5) * s, [127 * s, -127 * s]]).astype(np.float32)
+    W = row[None, :]
+    for rounding in (mj.ROUND_RHE, mj.ROUND_LEGACY):
+        q, sc = _quant_dev(W, dev, rounding)
+        ref = oracle.quantize_rowwise_rhe(W) if rounding == mj.ROUND_RHE else \
+            oracle.quantize_rowwise_legacy(W)
+        np.testing.assert_array_equal(q.cpu().numpy(), ref[0])
+        np.testing.assert_array_equal(sc.cpu().numpy(), ref[1])
+
+
+def test_quantize_symmetric_int8_per_tensor(oracle, dev):
+    x = oracle.randn_f32((257, 129), seed=3) * np.float32(3)
+    x[0, :6] = [0.49999997, -0.49999997, 2.5, -2.5, 1e6, -1e6]
+    for s in (0.0, 1.0, 0.05, 1.0 / 127):
+        got = mj.quantize_symmetric_int8(mj.Tensor(to_dev(x, dev)), s).numpy()
+        np.testing.assert_array_equal(got, oracle.quantize_symmetric_int8(x, s))
+
+
+def test_minmax_scale(oracle, dev):
+    x = oracle.randn_f32((1000, 37), seed=9)
+    x[5, 5] = -7.25
+    got = mj.functional.scale_symmetric_device(mj.Tensor(to_dev(x, dev)))
+    assert np.float32(got) == np.float32(oracle.minmax_scale_symmetric(x))
+    obs = mj.MinMaxObserver()
+    obs.observe(mj.Tensor(to_dev(x, dev)))
+    obs.observe(mj.Tensor(to_dev(x * 0.5, dev)))
+    assert np.float32(obs.scale_symmetric()) == np.float32(oracle.minmax_scale_symmetric(x))
+    zero = mj.functional.scale_symmetric_device(mj.Tensor(to_dev(np.zeros(10, np.float32), dev)))
+    assert zero == 1.0
+
+
+# ------------------------------------------------------------- int8 GEMM (legacy)
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (64, 64, 64), (37, 53, 80), (5, 7, 10), (200, 300, 1024),
+                                   (130, 129, 16)])
+def test_int8_gemm_bit_exact(oracle, dev, M, N, K):
+    rng = np.random.default_rng(M * N + K)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+    a = mj.Tensor(to_dev(A, dev))
+    w = mj.Tensor(to_dev(B, dev))
+    got = mj.matmul_i8_i8_to_i32(a, w.transpose()).numpy()
+    np.testing.assert_array_equal(got, oracle.matmul_i8_i8_to_i32(A, B))
+
+
+def test_int8_gemm_legacy_literal(oracle, dev):
+    """The reference's stride-ignoring read of w_q.transpose() (bug i):
+    result is A @ reshape(w_q.flat, [K, N])."""
+    rng = np.random.default_rng(5)
+    A = rng.integers(-128, 128, size=(3, 5), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(4, 5), dtype=np.int8)  # w_q [N=4, K=5]
+    got = mj.matmul_i8_i8_to_i32(mj.Tensor(to_dev(A, dev)), mj.Tensor(to_dev(B, dev)).transpose(),
+                                 legacy_literal=True).numpy()
+    ref = oracle.matmul_i8_i8_to_i32(A, B, legacy_literal=True)
+    np.testing.assert_array_equal(got, ref)
+    lit = A.astype(np.int32) @ B.reshape(5, 4).astype(np.int32)
+    np.testing.assert_array_equal(got, lit)
+    assert not np.array_equal(got, A.astype(np.int32) @ B.T.astype(np.int32))
+
+
+def test_dequantize(oracle, dev):
+    rng = np.random.default_rng(6)
+    acc = rng.integers(-2 ** 26, 2 ** 26, size=(33, 65), dtype=np.int32)
+    b = oracle.randu_f32((65,), -1, 1, seed=2)
+    got = mj.dequantize_i32_to_f32_add_bias(mj.Tensor(to_dev(acc, dev)), 3.0517578e-05,
+                                            mj.Tensor(to_dev(b, dev))).numpy()
+    np.testing.assert_array_equal(got, oracle.dequant_i32_bias(acc, np.float32(3.0517578e-05), b))
+
+
+@pytest.mark.parametrize("M,N,K,literal", [(256, 256, 256, False), (1, 11008, 4096, False),
+                                           (17, 40, 24, True), (64, 96, 100, False)])
+def test_quant_linear_bit_exact(oracle, dev, M, N, K, literal):
+    x = oracle.randn_f32((M, K), seed=M + 1)
+    W = oracle.randn_f32((N, K), std=0.02, seed=N + 2)
+    b = oracle.randu_f32((N,), -0.0625, 0.0625, seed=3)
+    s_x = oracle.minmax_scale_symmetric(x)
+    s_w = oracle.minmax_scale_symmetric(W)
+    Wq = oracle.quantize_symmetric_int8(W, s_w)
+    ql = mj.QuantLinear(K, N, mj.Tensor(to_dev(Wq, dev)), mj.Tensor(to_dev(b, dev)), s_w, s_x,
+                        legacy_literal=literal)
+    got = ql.forward(mj.Tensor(to_dev(x, dev))).numpy()
+    np.testing.assert_array_equal(got, oracle.quant_linear_fw(x, Wq, b, s_w, s_x, literal))
+
+
+def test_ptq_flow(oracle, dev):
+    """prepare -> calibrate -> convert -> Converted.forward on the
+    Linear(10,32) -> ReLU -> Linear(32,2) model of sequential_min.mojo."""
+    l1, l2 = mj.Linear(10, 32), mj.Linear(32, 2)
+    W1 = oracle.randn_f32((32, 10), std=0.3, seed=1)
+    W2 = oracle.randn_f32((2, 32), std=0.3, seed=2)
+    b1 = oracle.randu_f32((32,), -0.1, 0.1, seed=3)
+    b2 = oracle.randu_f32((2,), -0.1, 0.1, seed=4)
+    l1.weight.torch.copy_(torch.from_numpy(W1)); l1.bias_t.torch.copy_(torch.from_numpy(b1))
+    l2.weight.torch.copy_(torch.from_numpy(W2)); l2.bias_t.torch.copy_(torch.from_numpy(b2))
+    x = oracle.randn_f32((4, 10), seed=5)
+    p = mj.prepare(l1, mj.ReLU(), l2)
+    p.forward(mj.Tensor(to_dev(x, dev)))
+    conv = mj.convert(p)
+    got = conv.forward(mj.Tensor(to_dev(x, dev))).numpy()
+    # oracle: same flow on the CPU.  The ReLU-output scale comes from an fp32
+    # Linear, equal to the oracle's to rounding; the rest of the chain is
+    # then exact given that scale.
+    y1 = oracle.linear_fw_f32(x, W1, b1)
+    y2 = np.where(y1 > 0, y1, 0).astype(np.float32)
+    s_in = oracle.minmax_scale_symmetric(x)
+    s_w1, s_w2 = oracle.minmax_scale_symmetric(W1), oracle.minmax_scale_symmetric(W2)
+    assert np.float32(conv.q1.s_x) == np.float32(s_in)
+    assert np.float32(conv.q1.s_w) == np.float32(s_w1)
+    assert np.float32(conv.q2.s_w) == np.float32(s_w2)
+    assert abs(conv.q2.s_x - oracle.minmax_scale_symmetric(y2)) <= 1e-6 * conv.q2.s_x
+    s_relu = conv.q2.s_x
+    q1 = oracle.quant_linear_fw(x, oracle.quantize_symmetric_int8(W1, s_w1), b1, s_w1, s_in)
+    q1 = np.where(q1 > 0, q1, 0).astype(np.float32)
+    ref = oracle.quant_linear_fw(q1, oracle.quantize_symmetric_int8(W2, s_w2), b2, s_w2, s_relu)
+    np.testing.assert_array_equal(got, ref)
+
+
+# ------------------------------------------------------------- W8A16
+def _w8_case(oracle, dev, M, N, K, seed):
+    x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed))
+    W = oracle.randn_f32((N, K), std=0.02, seed=seed + 1)
+    Q, s = oracle.quantize_rowwise_rhe(W)
+    b = oracle.randu_f32((N,), -1.0 / 16, 1.0 / 16, seed=seed + 2)
+    return x, Q, s, b
+
+
+def test_c3_gemv(oracle, dev):
+    M, N, K = 1, 11008, 4096
+    x, Q, s, b = _w8_case(oracle, dev, M, N, K, 3)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev))
+    y = lin.forward(bf16_dev(x, dev))
+    _, ref = oracle.linear_w8a16(x, Q, s, b)
+    err = normwise_rel(bf16_host_f32(y), ref)
+    print(f"C3 gemv normwise rel err {err:.3e}", flush=True)
+    assert err <= BF16_TOL
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16)])
+def test_gemv_shapes(oracle, dev, M, N, K):
+    x, Q, s, b = _w8_case(oracle, dev, M, N, K, M * 100 + N)
+    for bias, epi in ((b, mj.EPI_NONE), (None, mj.EPI_GELU_TANH), (b, mj.EPI_SILU)):
+        lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev),
+                          None if bias is None else to_dev(bias, dev), epi)
+        y = lin.forward(bf16_dev(x, dev))
+        _, ref = oracle.linear_w8a16(x, Q, s, bias, epi)
+        assert normwise_rel(bf16_host_f32(y), ref) <= BF16_TOL
+
+
+def test_c4_prefill_gelu(oracle, dev):
+    M, N, K = 2048, 4096, 4096
+    x, Q, s, b = _w8_case(oracle, dev, M, N, K, 40)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_GELU_TANH)
+    y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    worst = 0.0
+    for r in (0, 1, 127, 128, 1023, 2046, 2047):
+        _, ref = oracle.linear_w8a16(x[r:r + 1], Q, s, b, mj.EPI_GELU_TANH)
+        worst = max(worst, normwise_rel(y[r:r + 1], ref))
+    print(f"C4 prefill worst normwise rel err {worst:.3e}", flush=True)
+    assert worst <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 64, 256), (100, 300, 1040), (257, 520, 512)])
+def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
+    x, Q, s, b = _w8_case(oracle, dev, M, N, K, M + N)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_RELU)
+    y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    _, ref = oracle.linear_w8a16(x, Q, s, b, mj.EPI_RELU)
+    assert normwise_rel(y, ref) <= BF16_TOL
+
+
+def _mlp_case(oracle, M, K, I, H, seed):
+    x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed))
+    Wg, sg = oracle.quantize_rowwise_rhe(oracle.randn_f32((I, K), std=0.02, seed=seed + 6))
+    Wu, su = oracle.quantize_rowwise_rhe(oracle.randn_f32((I, K), std=0.02, seed=seed + 7))
+    Wd, sd = oracle.quantize_rowwise_rhe(oracle.randn_f32((H, I), std=0.02, seed=seed + 8))
+    return x, Wg, sg, Wu, su, Wd, sd
+
+
+def _run_mlp(dev, x, Wg, sg, Wu, su, Wd, sd):
+    mk = lambda q, s: mj.W8Linear(to_dev(q, dev), to_dev(s, dev))
+    mlp = mj.W8MLP(mk(Wg, sg), mk(Wu, su), mk(Wd, sd))
+    y, h = mlp.forward(bf16_dev(x, dev))
+    return bf16_host_f32(y), bf16_host_f32(h)
+
+
+def test_c5_mlp(oracle, dev):
+    M, K, I, H = 512, 4096, 11008, 4096
+    case = _mlp_case(oracle, M, K, I, H, 0)
+    y, h = _run_mlp(dev, *case)
+    worst_h = worst_y = 0.0
+    for r in (0, 255, 256, 511):
+        hr, yr = oracle.mlp_w8a16(*case, rows=(r, r + 1))
+        worst_h = max(worst_h, normwise_rel(h[r:r + 1], oracle.bf16_to_f32(hr)))
+        worst_y = max(worst_y, normwise_rel(y[r:r + 1], oracle.bf16_to_f32(yr)))
+    print(f"C5 mlp worst normwise rel err h {worst_h:.3e} y {worst_y:.3e}", flush=True)
+    assert worst_h <= BF16_TOL and worst_y <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (40, 512, 256, 320), (300, 256, 528, 64)])
+def test_mlp_shapes(oracle, dev, M, K, I, H):
+    case = _mlp_case(oracle, M, K, I, H, M)
+    y, h = _run_mlp(dev, *case)
+    hr, yr = oracle.mlp_w8a16(*case)
+    assert normwise_rel(h, oracle.bf16_to_f32(hr)) <= BF16_TOL
+    assert normwise_rel(y, oracle.bf16_to_f32(yr)) <= BF16_TOL
