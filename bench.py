@@ -43,7 +43,8 @@ def _args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5)")
+    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,copy);"
+                   " copy is run only when named")
     return p.parse_args()
 
 
@@ -214,6 +215,21 @@ def bench_c1(steps, warmup):
     }
 
 
+def bench_copy(steps, warmup):
+    """A plain device copy of known size: the calibration point for the
+    rocprof FETCH_SIZE / WRITE_SIZE counters and the achievable HBM rate."""
+    import torch
+    n = 256 * 1024 * 1024 // 4  # 256 MiB per buffer
+    srcs = [torch.ones(n, device="cuda") for _ in range(2)]
+    dst = torch.empty(n, device="cuda")
+    ms = _time_launches(lambda i: dst.copy_(srcs[i % 2]), max(steps // 4, 10), warmup)
+    bytes_ = 2 * n * 4
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    return {"name": "copy_256MiB", "metric": "device copy GB/s (read+write)", "value": gbs,
+            "unit": "GB/s", "ms_per_launch": ms, "bytes_per_launch": bytes_,
+            "read_bytes": n * 4, "write_bytes": n * 4}
+
+
 def cpu_baseline_c2(rows: int = 128):
     """The oracle's strict-k fp32 dot on upcast bf16 inputs (momijo's CPU
     engine applied to bf16 data, single thread) over `rows` rows of C2."""
@@ -255,8 +271,8 @@ def main():
     print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
-                    ("c5", bench_c5), ("c1", bench_c1)):
-        if want(key):
+                    ("c5", bench_c5), ("c1", bench_c1), ("copy", bench_copy)):
+        if want(key) and (key != "copy" or "copy" in only):
             r = fn(a.steps, a.warmup)
             secondary.append(r)
             print(f"# {key} done: {r['value']:.1f} {r['unit']}", file=sys.stderr, flush=True)

@@ -1,0 +1,105 @@
+"""Host-side checks of the C ABI that need no GPU: the library loads, every
+function include/momijo_hip.h declares is exported and bound with a
+signature, the enum values agree between header, Python and oracle, and the
+argument validation returns the documented status codes before any device
+work is enqueued.  Plus the bench contract for --gpus > 1."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+from momijo_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_header_symbol_is_exported(lib):
+    syms = _lib.header_symbols()
+    assert len(syms) == len(set(syms)) >= 19
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(_lib.SIGNATURES), set(syms) ^ set(_lib.SIGNATURES)
+
+
+def test_exported_dynamic_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(mj_[a-z0-9_]+)\b", out))
+    assert set(_lib.header_symbols()) <= exported
+
+
+def _defines(prefix):
+    with open(_lib.HEADER_PATH) as f:
+        return {m[0]: int(m[1]) for m in re.findall(rf"#define ({prefix}\w+) (\d+)", f.read())}
+
+
+def test_enum_values_agree(oracle):
+    epi = _defines("MJ_EPI_")
+    assert epi == {"MJ_EPI_NONE": _lib.EPI_NONE, "MJ_EPI_RELU": _lib.EPI_RELU,
+                   "MJ_EPI_GELU_TANH": _lib.EPI_GELU_TANH, "MJ_EPI_SILU": _lib.EPI_SILU,
+                   "MJ_EPI_GELU_TANH_APPROX": _lib.EPI_GELU_TANH_APPROX,
+                   "MJ_EPI_SILU_APPROX": _lib.EPI_SILU_APPROX,
+                   "MJ_EPI_RELU_UNARY": _lib.EPI_RELU_UNARY}
+    for k, v in epi.items():
+        assert getattr(oracle, k[3:]) == v
+    st = _defines("MJ_ERR_")
+    assert st["MJ_ERR_ARG"] == _lib.MJ_ERR_ARG and st["MJ_ERR_ALLOC"] == _lib.MJ_ERR_ALLOC
+    assert _defines("MJ_ROUND_") == {"MJ_ROUND_RHE": 0, "MJ_ROUND_LEGACY": 1}
+
+
+def test_version_and_device_probe(lib):
+    assert lib.mj_version() == 100
+    assert lib.mj_device_available() in (0, 1)
+
+
+def _err(lib):
+    return lib.mj_last_error().decode()
+
+
+def test_validation_status_codes(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.mj_matmul_f32(-1, 2, 3, p, 3, 1, p, 2, 1, None, 0, p, 2, None) == _lib.MJ_ERR_ARG
+    assert "negative" in _err(lib)
+    assert lib.mj_matmul_f32(2, 2, 3, p, 3, 1, p, 2, 1, None, 99, p, 2, None) == _lib.MJ_ERR_ARG
+    assert lib.mj_matmul_f32(2, 4, 3, p, 3, 1, p, 4, 1, None, 0, p, 2, None) == _lib.MJ_ERR_SHAPE
+    assert lib.mj_matmul_f32(2, 4, 3, None, 3, 1, p, 4, 1, None, 0, p, 4, None) == _lib.MJ_ERR_ARG
+    assert lib.mj_gemm_bf16_nt(4, 4, 12, p, 12, p, 12, None, 0, p, 4, None) == _lib.MJ_ERR_UNSUPPORTED
+    assert lib.mj_gemm_bf16_nt(4, 4, 16, p, 8, p, 16, None, 0, p, 4, None) == _lib.MJ_ERR_SHAPE
+    assert lib.mj_linear_w8a16(p, p, p, None, 0, p, 1, 8, 24, None) == _lib.MJ_ERR_UNSUPPORTED
+    assert lib.mj_quantize_rowwise_i8(p, 4, 16, 7, p, p, None) == _lib.MJ_ERR_ARG
+    assert lib.mj_quantize_rowwise_i8(p, 4, 0, 0, p, p, None) == _lib.MJ_ERR_SHAPE
+    assert lib.mj_activation_f32(0, p, p, -1, None) == _lib.MJ_ERR_ARG
+    assert lib.mj_minmax_f32(p, 0, p, None) == _lib.MJ_ERR_ARG
+    assert lib.mj_mlp_w8a16(p, p, p, p, p, p, p, p, p, 4, 24, 16, 8, None) == _lib.MJ_ERR_UNSUPPORTED
+    big = 1 << 31
+    assert lib.mj_matmul_i8_i8_to_i32(p, p, p, big, 1, 1, 0, None) == _lib.MJ_ERR_UNSUPPORTED
+
+
+def test_empty_problems_are_noops(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.mj_matmul_f32(0, 5, 3, None, 3, 1, None, 5, 1, None, 0, p, 5, None) == _lib.MJ_OK
+    assert lib.mj_gemm_bf16_nt(4, 0, 16, None, 16, None, 16, None, 0, p, 0, None) == _lib.MJ_OK
+    assert lib.mj_linear_w8a16(None, None, None, None, 0, None, 0, 8, 16, None) == _lib.MJ_OK
+    assert lib.mj_activation_f32(0, None, None, 0, None) == _lib.MJ_OK
+    assert lib.mj_launch_linear_fw_h(None, None, None, None, 0, 4, 4, 0) == _lib.MJ_OK
+
+
+def test_python_layer_raises_on_status():
+    with pytest.raises(_lib.MomijoHipError) as e:
+        _lib.call("mj_activation_f32", 42, None, None, 1, None)
+    assert e.value.status == _lib.MJ_ERR_ARG
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "single-GPU" in r.stdout
