@@ -114,6 +114,13 @@ def bench_c3(steps, warmup):
     hot_ms = _time_launches(lambda i: lins[0].forward(x, out=y), n_launch, max(warmup, 16))
     bytes_ = N * K + N * 4 + K * 2 + N * 4 + N * 2   # Q + scales + x + bias(f32) + y
     gbs = bytes_ / (ms * 1e-3) / 1e9
+    # the device-side cost of one dispatch of this kernel over 4 rows: a floor
+    # that every launch pays whatever its size
+    x4 = torch.empty((1, 4), dtype=torch.bfloat16, device="cuda")
+    tiny = mj.W8Linear(q0[:4].contiguous(), s[:4].contiguous(), bias[:4].contiguous())
+    y4 = torch.empty((1, 4), dtype=torch.bfloat16, device="cuda")
+    floor_ms = _time_launches(lambda i: tiny.forward(x[:, :K], out=y4), n_launch, 16)
+    del x4
     return {
         "name": "c3_int8_gemv_11008x4096",
         "metric": "int8 weight-only GEMV GB/s (M=1)",
@@ -123,6 +130,8 @@ def bench_c3(steps, warmup):
         "bytes_per_launch": bytes_,
         "weights_rotated_over": copies,
         "cache_hot_GBs": bytes_ / (hot_ms * 1e-3) / 1e9,
+        "dispatch_floor_us": floor_ms * 1e3,
+        "streaming_GBs_excluding_floor": bytes_ / ((ms - floor_ms) * 1e-3) / 1e9,
     }
 
 

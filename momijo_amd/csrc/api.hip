@@ -44,6 +44,22 @@ int32_t check_dims(int64_t M, int64_t N, int64_t K) {
 
 hipStream_t S(void *stream) { return (hipStream_t)stream; }
 
+// Plans and launches an NT GEMM, with a stream-ordered fp32 workspace when the
+// plan splits K.
+int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
+  const mj::GemmPlan plan = mj::plan_gemm_nt(p);
+  const size_t ws = plan.workspace_bytes(p);
+  if (ws) {
+    if (hipMallocAsync((void **)&p.part, ws, stream) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(MJ_ERR_ALLOC, "%s: split-K workspace allocation failed", what);
+    }
+  }
+  int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+  if (ws) (void)hipFreeAsync(p.part, stream);
+  return st;
+}
+
 }  // namespace
 
 extern "C" {
@@ -150,7 +166,7 @@ int32_t mj_gemm_bf16_nt(int64_t M, int64_t N, int64_t K, const uint16_t *A, int6
   mj::GemmNT p;
   p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.bias = bias; p.epi = epilogue;
   p.C = C; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.bkind = mj::B_BF16;
-  return hip_status(mj::launch_gemm_nt(p, S(stream)), "gemm_bf16 launch");
+  return run_gemm_nt(p, S(stream), "gemm_bf16");
 }
 
 // ------------------------------------------------------------------ int8 legacy
@@ -275,7 +291,7 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
   mj::GemmNT p;
   p.A = x; p.lda = K; p.B = Q; p.ldb = K; p.scales = scales; p.bias = bias; p.epi = epilogue;
   p.C = y; p.ldc = N; p.M = M; p.N = N; p.K = K; p.bkind = mj::B_INT8;
-  return hip_status(mj::launch_gemm_nt(p, S(stream)), "gemm_w8a16 launch");
+  return run_gemm_nt(p, S(stream), "gemm_w8a16");
 }
 
 int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const int8_t *Wu,
@@ -292,7 +308,7 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   mj::GemmNT gu;
   gu.A = x; gu.lda = K; gu.B = Wg; gu.B2 = Wu; gu.ldb = K; gu.scales = sg; gu.scales2 = su;
   gu.C = h; gu.ldc = I; gu.M = M; gu.N = I; gu.K = K; gu.bkind = mj::B_INT8; gu.gate_up = true;
-  if (int32_t st = hip_status(mj::launch_gemm_nt(gu, S(stream)), "gate/up launch")) return st;
+  if (int32_t st = run_gemm_nt(gu, S(stream), "gate/up")) return st;
   if (M <= 8)
     return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
                                             S(stream)),
@@ -300,7 +316,7 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   mj::GemmNT dn;
   dn.A = h; dn.lda = I; dn.B = Wd; dn.ldb = I; dn.scales = sd; dn.C = y; dn.ldc = H;
   dn.M = M; dn.N = H; dn.K = I; dn.bkind = mj::B_INT8;
-  return hip_status(mj::launch_gemm_nt(dn, S(stream)), "down launch");
+  return run_gemm_nt(dn, S(stream), "down");
 }
 
 }  // extern "C"

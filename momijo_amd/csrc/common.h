@@ -14,6 +14,22 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 
+// Buffer resource over [base, base + bytes) for raw buffer loads: a load whose
+// byte offset lies outside the range returns zero, which gives branch-free
+// zero fill at matrix edges.  bytes is clamped to the 31-bit offset range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int32_t n = bytes > 0x7FFFFFF0LL ? 0x7FFFFFF0 : (int32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+// An offset no resource above ever covers: loads from it return zero.
+constexpr uint32_t kOobOffset = 0x7FFFFFF0u;
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // 16-byte streaming load (nontemporal: the data is read once).
 __device__ __forceinline__ uint4 load_nt16(const void *p) {
   const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);

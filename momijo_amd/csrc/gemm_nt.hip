@@ -1,37 +1,53 @@
 // NT GEMM on gfx950 bf16 MFMA: C[M,N] = epi((A[M,K] . B[N,K]^T) * s[n] + b[n]).
 //
-// A is bf16, B is bf16 or int8 (per-output-channel quantized weights); both
-// are K-contiguous, the layout of momijo's Linear weight [OutF, InF]
-// (learn/nn/layers.mojo:347-348), so every global load is a 16-byte run of K.
+// A is bf16 activations, B is bf16 or int8 (per-output-channel quantized)
+// weights; both are K-contiguous, the layout of momijo's Linear weight
+// [OutF, InF] (learn/nn/layers.mojo:347-348), so every global load is a
+// 16-byte run of K.
 //
-// Structure (one workgroup = 4 waves = 256 threads per BM x BN tile):
-//  * global -> registers -> LDS, double-buffered with one barrier per 64-wide
-//    K step: the next K step's loads are in flight while the current one is
-//    multiplied.  int8 weights are converted to bf16 (exactly: |q| <= 127) on
-//    their way into LDS, so the MFMA loop is the same for both weight types.
-//  * LDS rows are padded to 72 bf16 (144 B): the 16-byte fragment reads of 16
-//    consecutive lanes then fall into distinct banks.
-//  * each wave owns a (BM/2) x (BN/2) quarter of the tile and runs
-//    v_mfma_f32_32x32x16_bf16 over it: lane l feeds row (l%32) of A and row
-//    (l%32) of B with 8 consecutive K values, and receives 16 accumulators
-//    at rows 8*(r/4) + 4*(l/32) + r%4, column l%32.
-//  * the epilogue applies the per-column weight scale, the bias and the
-//    activation in fp32 (no FMA contraction, as in the reference), rounds to
-//    bf16 (RNE) and stores.
-//  * gate/up mode (the Llama-style FFN): each wave's B rows hold 64 gate rows
-//    followed by the 64 up rows of the same output columns, so one lane holds
-//    g and u for the same (m, n) and writes silu(g*sg)*(u*su) directly.
+// One workgroup = 8 waves (2 per SIMD) per BM x BN output tile:
+//  * two waves share each SIMD, so one wave's LDS / global waits are covered by
+//    the other's MFMAs; waves are laid out 2 (M) x 4 (N), each owning a
+//    (BM/2) x (BN/4) sub-tile (128 x 64 for the 256 x 256 tile) of
+//    v_mfma_f32_32x32x16_bf16 accumulators;
+//  * K advances 64 at a time through two LDS stages; the next stage's bf16
+//    tiles go from HBM straight into LDS (buffer_load ... lds: no staging
+//    registers, no ds_write), issued before the current stage's MFMAs;
+//    int8 weight tiles take the register path and are widened to bf16
+//    (exactly, |q| <= 127) on their way into LDS, so the MFMA loop is the
+//    same for both weight types;
+//  * raw buffer loads return zero for offsets outside their resource: edge
+//    tiles (rows >= M, chunks >= K) need no branches;
+//  * LDS rows are 64 bf16 (128 B) with an XOR swizzle (see swz) that keeps
+//    both the 1-KB direct loads and the 16-byte fragment reads free of bank
+//    conflicts;
+//  * MFMA operands are swapped (the weight tile feeds the A operand), so a
+//    lane's 16 accumulators are 4 runs of 4 consecutive output columns of one
+//    output row, stored as 8-byte runs;
+//  * the epilogue (per-column weight scale, bias, activation in fp32 with no
+//    FMA contraction, RNE to bf16) is instantiated per activation;
+//  * gate/up mode (Llama FFN): each wave's B rows are WN/2 gate rows then the
+//    WN/2 up rows of the same output columns, so one lane holds g and u for
+//    the same (m, n) and writes silu32(g*sg) * (u*su) directly;
+//  * split-K (when the tile grid alone cannot fill the 256 CUs): workgroup
+//    (split, tile) accumulates its K slice into an fp32 partial buffer and a
+//    second kernel sums the partials in split order and applies the epilogue.
+//  * workgroup ids are remapped so the 32 workgroups of one XCD form a
+//    compact block of tiles sharing that XCD's L2 (tile_coords).
 #include "common.h"
 #include "launch.h"
 
 namespace mj {
 
-constexpr int kBK = 64;        // K per pipeline stage
-constexpr int kLds = kBK + 8;  // LDS row stride in bf16 elements (144 B)
+constexpr int kBK = 64;  // K per pipeline stage
 
-template <int BM, int BN>
-constexpr size_t gemm_nt_lds_bytes() {
-  return size_t(2) * (BM + BN) * kLds * sizeof(uint16_t);
+__device__ __forceinline__ float epi_scale_bias(float acc, float s, float b, bool has_s,
+                                                bool has_b) {
+#pragma clang fp contract(off)
+  float v = acc;
+  if (has_s) v = v * s;
+  if (has_b) v = v + b;
+  return v;
 }
 
 // int8 x16 (one 16-byte word) -> 16 bf16 (exact), as two 16-byte words.
@@ -52,111 +68,246 @@ __device__ __forceinline__ void i8x16_to_bf16x16(const uint4 &q, uint4 &lo, uint
   hi = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-__device__ __forceinline__ float epi_scale_bias(float acc, float s, float b, bool has_s,
-                                                bool has_b) {
+
+// LDS is 64 banks x 4 B, and a 16-byte access is served 16 lanes at a time:
+// a 256-byte bank window holds two 128-byte rows, so 16 consecutive rows
+// read at one logical chunk must land on 16 distinct 16-byte slots.  XOR-ing
+// the chunk with (row / 2) % 8 gives the 8 even rows 8 distinct slots in the
+// first half of the window and the 8 odd rows 8 in the second half.
+__device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ ((row >> 1) & 7)) * 8; }
+
+// Stores 4 consecutive output columns [nb, nb+4) of row m.
+__device__ __forceinline__ void store4_bf16(const GemmNT &p, int m, int nb, const float v[4]) {
+  uint16_t *dst = p.C + (size_t)m * p.ldc + nb;
+  if (nb + 3 < (int)p.N && (p.ldc & 3) == 0 && ((uintptr_t)p.C & 7) == 0) {
+    *(uint2 *)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (nb + q < (int)p.N) dst[q] = (uint16_t)f32_to_bf16_bits(v[q]);
+  }
+}
+
+// Epilogue of the gen2 kernel for one activation E: scale, bias, E, bf16.
+template <int E, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_tile8(const GemmNT &p, const f32x16 (&acc)[TM][TN], int m0,
+                                            int n0, int wm, int wn, int lane) {
+  const int M = (int)p.M, N = (int)p.N;
+  const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nb = n0 + wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+      float s[4], b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = nb + q < N ? nb + q : N - 1;
+        s[q] = has_s ? p.scales[n] : 1.0f;
+        b[q] = has_b ? p.bias[n] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[q] = apply_epi(E, epi_scale_bias(acc[i][j][4 * g + q], s[q], b[q], has_s, has_b));
+        if (m < M) store4_bf16(p, m, nb, v);
+      }
+    }
+  }
+}
+
+// Gate/up epilogue: subtile 0 is the gate, subtile 1 the up projection of the
+// same output columns; h = silu32(g * sg) * (u * su).
+template <int TM, int WM, int WN>
+__device__ __forceinline__ void store_gateup8(const GemmNT &p, const f32x16 (&acc)[TM][2], int m0,
+                                              int n0, int wm, int wn, int lane) {
+  const int M = (int)p.M, N = (int)p.N;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int nb = n0 + wn * (WN / 2) + 8 * g + 4 * (lane >> 5);
+    float sg[4], su[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + q < N ? nb + q : N - 1;
+      sg[q] = p.scales[n];
+      su[q] = p.scales2[n];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WM + i * 32 + (lane & 31);
+      float h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float gv = epi_scale_bias(acc[i][0][4 * g + q], sg[q], 0.0f, true, false);
+        const float uv = epi_scale_bias(acc[i][1][4 * g + q], su[q], 0.0f, true, false);
+        {
 #pragma clang fp contract(off)
-  float v = acc;
-  if (has_s) v = v * s;
-  if (has_b) v = v + b;
-  return v;
+          h[q] = silu32(gv) * uv;
+        }
+      }
+      if (m < M) store4_bf16(p, m, nb, h);
+    }
+  }
+}
+
+// Split-K: raw fp32 sums of this workgroup's K slice, 4 columns per store.
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_part8(const GemmNT &p, const f32x16 (&acc)[TM][TN], int m0,
+                                            int n0, int wm, int wn, int lane, int split) {
+  const int M = (int)p.M, N = (int)p.N;
+  float *part = p.part + (size_t)split * M * N;
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nb = n0 + wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        if (m >= M) continue;
+        float *dst = part + (size_t)m * N + nb;
+        if (vec && nb + 3 < N) {
+          *(float4 *)dst = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1],
+                                       acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nb + q < N) dst[q] = acc[i][j][4 * g + q];
+        }
+      }
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds_dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_dst, 16, off, 0, 0, 0);
 }
 
 template <int BM, int BN, int BKIND, bool GATEUP>
-__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmNT p) {
-  constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile
+__global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
+  constexpr int WGM = 2, WGN = 4;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;  // output columns per tile
-  constexpr int A_LOADS = BM / 32;              // 16-B chunks per thread
-  constexpr int B_LOADS = BKIND == B_BF16 ? BN / 32 : BN / 64;
-  static_assert(!GATEUP || TN % 2 == 0, "gate/up needs an even number of N subtiles");
+  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
+  constexpr int A_DMA = BM / 64;                         // 1-KB loads per wave per stage
+  constexpr int B_DMA = BKIND == B_BF16 ? BN / 64 : 0;
+  constexpr int B_REG = BKIND == B_BF16 ? 0 : BN * 4 / 512;  // int8: 16-B chunks per thread
+  static_assert(!GATEUP || TN == 2, "gate/up pairs one gate and one up subtile per wave");
+  static_assert(A_DMA >= 1, "tile too small");
 
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t *As = lds;                          // [2][BM][kLds]
-  uint16_t *Bs = lds + 2 * BM * kLds;          // [2][BN][kLds]
+  uint16_t *As = lds;                    // [2][BM][64]
+  uint16_t *Bs = lds + 2 * BM * kBK;     // [2][BN][64]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
-  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  const int M = (int)p.M, N = (int)p.N;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN_OUT - 1) / BN_OUT;
+  const int tiles = tiles_m * tiles_n;
+  const int split = blockIdx.x / tiles;
   int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, 4, tm, tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN_OUT;
+  // this workgroup's K slice: stages [kt0, kt1); loads stop at K (edge) or at
+  // the slice end, whichever is first
+  const int nk_all = ((int)p.K + kBK - 1) / kBK;
+  const int per = (nk_all + p.splits - 1) / p.splits;
+  const int kt0 = split * per;
+  const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
+  const int K = kt1 * kBK < (int)p.K ? kt1 * kBK : (int)p.K;
 
-  // ---- global load addressing ------------------------------------------
-  // A: 8 chunks of 8 bf16 per 64-wide row; thread -> (row t/8 + 32 i, chunk t%8)
-  const int a_c = tid & 7;
-  const int a_r = tid >> 3;
-  const uint16_t *a_ptr[A_LOADS];
-  bool a_ok[A_LOADS];
+  // ---- A: direct loads.  Block b = i*8 + wave covers tile rows [8b, 8b+8).
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(p.A + (size_t)m0 * p.lda,
+                                              ((int64_t)(M - m0) * p.lda) * 2);
+  uint32_t a_off[A_DMA];
+  int a_kc[A_DMA];  // logical chunk (of 8 bf16) this lane fetches
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) {
-    const int m = m0 + a_r + 32 * i;
-    a_ok[i] = m < M;
-    a_ptr[i] = p.A + (size_t)(a_ok[i] ? m : 0) * p.lda + a_c * 8;
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (i * 8 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_kc[i] = c;
+    a_off[i] = (m0 + r < M) ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
   }
-  // B rows: bf16 -> 8 chunks/row like A; int8 -> 4 chunks of 16 per row.
-  constexpr int B_CPR = BKIND == B_BF16 ? 8 : 4;  // chunks per row
-  constexpr int B_RPP = 256 / B_CPR;              // rows per pass
-  const int b_c = tid % B_CPR;
-  const int b_r = tid / B_CPR;
-  const char *b_ptr[B_LOADS];
-  bool b_ok[B_LOADS];
+  // ---- B
   constexpr int ESZ = BKIND == B_BF16 ? 2 : 1;
-#pragma unroll
-  for (int i = 0; i < B_LOADS; ++i) {
-    const int r = b_r + B_RPP * i;  // row of the LDS B tile
-    int n;
-    const void *base = p.B;
+  const size_t b_base = (size_t)n0 * p.ldb * ESZ;
+  const int64_t b_bytes = (int64_t)(N - n0) * p.ldb * ESZ;
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc((const char *)p.B + b_base, b_bytes);
+  const __amdgpu_buffer_rsrc_t rB2 =
+      make_rsrc((const char *)(GATEUP ? p.B2 : p.B) + b_base, b_bytes);
+  auto b_src_row = [&](int r, bool &up) {  // LDS B row -> weight row (and which matrix)
+    up = false;
     if (GATEUP) {
-      // wave half wn = r / (BN/2); inside it 32*TN/2 gate rows then up rows
-      const int half = r / (BN / 2);
-      const int rr = r % (BN / 2);
-      const int up = rr / (BN / 4);
-      n = n0 + half * (BN / 4) + rr % (BN / 4);
-      base = up ? p.B2 : p.B;
-    } else {
-      n = n0 + r;
+      const int w = r / WN, rr = r % WN;
+      up = rr >= WN / 2;
+      return n0 + w * (WN / 2) + rr % (WN / 2);
     }
-    b_ok[i] = n < N;
-    b_ptr[i] = (const char *)base + ((size_t)(b_ok[i] ? n : 0) * p.ldb + b_c * (16 / ESZ)) * ESZ;
+    return n0 + r;
+  };
+  uint32_t b_off[B_DMA > 0 ? B_DMA : 1];
+  int b_kc[B_DMA > 0 ? B_DMA : 1];
+  bool b_up[B_DMA > 0 ? B_DMA : 1];
+#pragma unroll
+  for (int i = 0; i < B_DMA; ++i) {
+    const int r = (i * 8 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int n = b_src_row(r, b_up[i]);
+    b_kc[i] = c;
+    b_off[i] = n < N ? (uint32_t)(((size_t)(n - n0) * p.ldb + c * 8) * 2) : kOobOffset;
   }
-
-  uint4 ra[A_LOADS];
-  uint4 rb[B_LOADS];
-  auto load_stage = [&](int k0) {
+  // int8 register path: 4 chunks of 16 per 64-wide row
+  const int q_c = tid & 3, q_r = tid >> 2;
+  uint32_t q_off[B_REG > 0 ? B_REG : 1];
+  bool q_up[B_REG > 0 ? B_REG : 1];
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const bool ok = a_ok[i] && (k0 + a_c * 8 < K);
-      ra[i] = ok ? *(const uint4 *)(a_ptr[i] + k0) : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < B_REG; ++i) {
+    const int r = q_r + 128 * i;
+    const int n = b_src_row(r, q_up[i]);
+    q_off[i] = n < N ? (uint32_t)((size_t)(n - n0) * p.ldb + q_c * 16) : kOobOffset;
+  }
+  uint4 rq[B_REG > 0 ? B_REG : 1];
+
+  auto issue_stage = [&](int k0, int buf) {
+    uint16_t *as = As + buf * BM * kBK;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const bool ok = k0 + a_kc[i] * 8 < K;
+      dma16(rA, as + (i * 8 + wave) * 8 * kBK, ok ? a_off[i] + k0 * 2 : kOobOffset);
+    }
+    uint16_t *bs = Bs + buf * BN * kBK;
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const bool ok = k0 + b_kc[i] * 8 < K;
+      const uint32_t off = ok ? b_off[i] + k0 * 2 : kOobOffset;
+      if (GATEUP && b_up[i]) dma16(rB2, bs + (i * 8 + wave) * 8 * kBK, off);
+      else dma16(rB, bs + (i * 8 + wave) * 8 * kBK, off);
     }
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const bool ok = b_ok[i] && (k0 + b_c * (16 / ESZ) < K);
-      rb[i] = ok ? *(const uint4 *)(b_ptr[i] + (size_t)k0 * ESZ) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < B_REG; ++i) {
+      const bool ok = k0 + q_c * 16 < K;
+      const uint32_t off = ok ? q_off[i] + k0 : kOobOffset;
+      rq[i] = (GATEUP && q_up[i]) ? buffer_load16(rB2, off) : buffer_load16(rB, off);
     }
   };
-  auto store_stage = [&](int buf) {
-    uint16_t *as = As + buf * BM * kLds;
-    uint16_t *bs = Bs + buf * BN * kLds;
+  auto store_int8 = [&](int buf) {
+    uint16_t *bs = Bs + buf * BN * kBK;
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      *(uint4 *)(as + (a_r + 32 * i) * kLds + a_c * 8) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int r = b_r + B_RPP * i;
-      if (BKIND == B_BF16) {
-        *(uint4 *)(bs + r * kLds + b_c * 8) = rb[i];
-      } else {
-        uint4 lo, hi;
-        i8x16_to_bf16x16(rb[i], lo, hi);
-        *(uint4 *)(bs + r * kLds + b_c * 16) = lo;
-        *(uint4 *)(bs + r * kLds + b_c * 16 + 8) = hi;
-      }
+    for (int i = 0; i < B_REG; ++i) {
+      const int r = q_r + 128 * i;
+      uint4 lo, hi;
+      i8x16_to_bf16x16(rq[i], lo, hi);
+      *(uint4 *)(bs + r * kBK + swz(r, 2 * q_c)) = lo;
+      *(uint4 *)(bs + r * kBK + swz(r, 2 * q_c + 1)) = hi;
     }
   };
 
@@ -168,86 +319,119 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmNT p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nk = (K + kBK - 1) / kBK;
-  load_stage(0);
-  store_stage(0);
+  issue_stage(kt0 * kBK, 0);
+  if constexpr (B_REG > 0) store_int8(0);
   __syncthreads();
 
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_stage((kt + 1) * kBK);
-    const uint16_t *as = As + buf * BM * kLds + (wm * WM + frag_row) * kLds + frag_k;
-    const uint16_t *bs = Bs + buf * BN * kLds + (wn * WN + frag_row) * kLds + frag_k;
+  const int fr = lane & 31;
+  const int fh = lane >> 5;
+  const int sw = (lane >> 1) & 7;
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int buf = (kt - kt0) & 1;
+    // the other buffer was last read in stage kt-1, which every wave finished
+    // before the barrier that ended it
+    issue_stage((kt + 1) * kBK, buf ^ 1);
+    const uint16_t *as = As + buf * BM * kBK + (wm * WM + fr) * kBK;
+    const uint16_t *bs = Bs + buf * BN * kBK + (wn * WN + fr) * kBK;
+    bf16x8 fa[2][TM], fb[2][TN];
+    auto read_frags = [&](int slot, int ks) {
+      const int col = ((ks * 2 + fh) ^ sw) * 8;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[slot][i] = *(const bf16x8 *)(as + i * 32 * kBK + col);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[slot][j] = *(const bf16x8 *)(bs + j * 32 * kBK + col);
+    };
+    read_frags(0, 0);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = *(const bf16x8 *)(as + i * 32 * kLds + ks * 16);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = *(const bf16x8 *)(bs + j * 32 * kLds + ks * 16);
+      if (ks + 1 < kBK / 16) read_frags((ks + 1) & 1, ks + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i],
+                                                              acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) store_stage(buf ^ 1);
+    if constexpr (B_REG > 0) store_int8(buf ^ 1);
+    // the direct loads of stage kt+1 must have landed in LDS before anyone
+    // reads them: wait for this wave's loads, then the barrier covers all
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
   }
 
-  // ---- epilogue ---------------------------------------------------------
-  const int row_base = m0 + wm * WM + 4 * (lane >> 5);
-  if (!GATEUP) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * WN + j * 32 + (lane & 31);
-      if (n >= N) continue;
-      const float s = p.scales ? p.scales[n] : 1.0f;
-      const float b = p.bias ? p.bias[n] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (m < M) {
-            float v = epi_scale_bias(acc[i][j][r], s, b, p.scales != nullptr, p.bias != nullptr);
-            v = apply_epi(p.epi, v);
-            p.C[(size_t)m * p.ldc + n] = (uint16_t)f32_to_bf16_bits(v);
-          }
-        }
+  if (p.part != nullptr) {
+    if constexpr (!GATEUP) store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, split);
+    return;
+  }
+  if constexpr (!GATEUP) {
+    switch (p.epi) {
+      case EPI_RELU: store_tile8<EPI_RELU, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_GELU_TANH:
+        store_tile8<EPI_GELU_TANH, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_SILU: store_tile8<EPI_SILU, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_GELU_TANH_APPROX:
+        store_tile8<EPI_GELU_TANH_APPROX, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_SILU_APPROX:
+        store_tile8<EPI_SILU_APPROX, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_RELU_UNARY:
+        store_tile8<EPI_RELU_UNARY, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      default: store_tile8<EPI_NONE, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
     }
   } else {
-#pragma unroll
-    for (int j = 0; j < TN / 2; ++j) {
-      const int n = n0 + wn * (WN / 2) + j * 32 + (lane & 31);
-      if (n >= N) continue;
-      const float sg = p.scales[n];
-      const float su = p.scales2[n];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (m < M) {
-            const float g = epi_scale_bias(acc[i][j][r], sg, 0.0f, true, false);
-            const float u = epi_scale_bias(acc[i][j + TN / 2][r], su, 0.0f, true, false);
-            float h;
-            {
-#pragma clang fp contract(off)
-              h = silu32(g) * u;
-            }
-            p.C[(size_t)m * p.ldc + n] = (uint16_t)f32_to_bf16_bits(h);
-          }
-        }
-    }
+    store_gateup8<TM, WM, WN>(p, acc, m0, n0, wm, wn, lane);
   }
 }
 
+// Sums the split-K partials in split order and applies scale, bias, the
+// activation and the bf16 rounding; 4 columns per thread.
+template <int E>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
+  const int M = (int)p.M, N = (int)p.N;
+  const int n4 = (N + 3) / 4;
+  const int64_t total = (int64_t)M * n4;
+  const size_t plane = (size_t)M * N;
+  const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(t / n4);
+    const int nb = (int)(t - (int64_t)m * n4) * 4;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + q < N ? nb + q : N - 1;
+      float acc = 0.0f;
+      for (int s = 0; s < p.splits; ++s) acc += p.part[s * plane + (size_t)m * N + n];
+      v[q] = apply_epi(E, epi_scale_bias(acc, has_s ? p.scales[n] : 1.0f,
+                                         has_b ? p.bias[n] : 0.0f, has_s, has_b));
+    }
+    store4_bf16(p, m, nb, v);
+  }
+}
+
+static hipError_t launch_reduce(const GemmNT &p, hipStream_t stream) {
+  const int64_t total = p.M * ((p.N + 3) / 4);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  const dim3 g((unsigned)blocks), b(256);
+  switch (p.epi) {
+    case EPI_RELU: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RELU>, g, b, 0, stream, p); break;
+    case EPI_GELU_TANH:
+      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_GELU_TANH>, g, b, 0, stream, p); break;
+    case EPI_SILU: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_SILU>, g, b, 0, stream, p); break;
+    case EPI_GELU_TANH_APPROX:
+      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_GELU_TANH_APPROX>, g, b, 0, stream, p); break;
+    case EPI_SILU_APPROX:
+      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_SILU_APPROX>, g, b, 0, stream, p); break;
+    case EPI_RELU_UNARY:
+      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RELU_UNARY>, g, b, 0, stream, p); break;
+    default: hipLaunchKernelGGL(splitk_reduce_kernel<EPI_NONE>, g, b, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BKIND, bool GATEUP>
-static hipError_t launch_cfg(const GemmNT &p, hipStream_t stream) {
-  constexpr size_t lds = gemm_nt_lds_bytes<BM, BN>();
+static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
+  constexpr size_t lds = size_t(2) * (BM + BN) * kBK * sizeof(uint16_t);
   auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -258,30 +442,83 @@ static hipError_t launch_cfg(const GemmNT &p, hipStream_t stream) {
   }
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   const int tiles = (int)((p.M + BM - 1) / BM) * (int)((p.N + BN_OUT - 1) / BN_OUT);
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(256), lds, stream, p);
+  hipLaunchKernelGGL(kern, dim3(tiles * p.splits), dim3(512), lds, stream, p);
   return hipGetLastError();
 }
 
-// Picks the tile that keeps the 256 CUs busiest: the largest tile whose
-// grid still covers about one full wave of workgroups.
-hipError_t launch_gemm_nt(const GemmNT &p, hipStream_t stream) {
-  auto tiles = [&](int bm, int bn) {
-    return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  };
+template <int BKIND>
+static hipError_t launch_plain(int bm, int bn, const GemmNT &p, hipStream_t stream) {
+  if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false>(p, stream);
+  if (bm == 256 && bn == 128) return launch_tile<256, 128, BKIND, false>(p, stream);
+  if (bm == 128 && bn == 256) return launch_tile<128, 256, BKIND, false>(p, stream);
+  return launch_tile<128, 128, BKIND, false>(p, stream);
+}
+
+// Chooses the tile shape and K split.  Model: a shape's relative MFMA
+// efficiency times the fraction of CU slots its grid keeps busy (a 128 x 128
+// tile uses 64 KB of LDS, so two workgroups share a CU; the larger tiles need
+// one CU each), divided by the cost of the split-K partial round trip
+// (8 B per output and split, mostly MALL-resident, against 2K flops per output).
+// The efficiencies are measured at the BASELINE shapes on MI355X.
+GemmPlan plan_gemm_nt(const GemmNT &p) {
+  GemmPlan pl;
+  auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
   if (p.gate_up) {
-    // output columns per tile are BN/2
-    if (tiles(128, 128) >= 200 || p.M > 128)
-      return launch_cfg<128, 256, B_INT8, true>(p, stream);
-    return launch_cfg<128, 128, B_INT8, true>(p, stream);
+    // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up
+    pl.bm = p.M > 128 ? 256 : 128;
+    pl.bn = 256;
+    return pl;
   }
-  if (p.bkind == B_BF16) {
-    if (tiles(256, 256) >= 224) return launch_cfg<256, 256, B_BF16, false>(p, stream);
-    if (tiles(128, 256) >= 224) return launch_cfg<128, 256, B_BF16, false>(p, stream);
-    return launch_cfg<128, 128, B_BF16, false>(p, stream);
+  constexpr int kCUs = 256;
+  const int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+  const int per_cu[4] = {1, 1, 1, 2};
+  const double eff_bf16[4] = {1.0, 0.93, 0.95, 0.90};
+  const double eff_int8[4] = {1.0, 0.93, 0.95, 0.98};
+  const double *eff = p.bkind == B_BF16 ? eff_bf16 : eff_int8;
+  const int64_t nk = (p.K + kBK - 1) / kBK;
+  double best = -1.0;
+  for (int s = 0; s < 4; ++s) {
+    const int64_t t = tiles(shapes[s][0], shapes[s][1]);
+    const int64_t cap = (int64_t)kCUs * per_cu[s];
+    auto util = [&](int64_t n) { return (double)n / (double)(((n + cap - 1) / cap) * cap); };
+    double score = eff[s] * util(t);
+    int splits = 1;
+    if (t < cap) {
+      int sk = (int)((cap + t - 1) / t);
+      while (sk > 1 && nk / sk < 8) --sk;  // keep >= 8 stages per split
+      if (sk > 1) {
+        const double s2 = eff[s] * util(t * sk) / (1.0 + (double)sk * 150.0 / (double)p.K);
+        if (s2 > score) {
+          score = s2;
+          splits = sk;
+        }
+      }
+    }
+    if (score > best) {
+      best = score;
+      pl.bm = shapes[s][0];
+      pl.bn = shapes[s][1];
+      pl.splits = splits;
+    }
   }
-  if (tiles(256, 256) >= 224) return launch_cfg<256, 256, B_INT8, false>(p, stream);
-  if (tiles(128, 256) >= 224) return launch_cfg<128, 256, B_INT8, false>(p, stream);
-  return launch_cfg<128, 128, B_INT8, false>(p, stream);
+  return pl;
+}
+
+hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t stream) {
+  GemmNT p = p_in;
+  p.splits = pl.splits;
+  if (p.gate_up) {
+    p.splits = 1;
+    p.part = nullptr;
+    if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true>(p, stream);
+    return launch_tile<128, 256, B_INT8, true>(p, stream);
+  }
+  if (pl.splits > 1 && p.part == nullptr) return hipErrorInvalidValue;
+  if (pl.splits == 1) p.part = nullptr;
+  const hipError_t e = p.bkind == B_BF16 ? launch_plain<B_BF16>(pl.bm, pl.bn, p, stream)
+                                         : launch_plain<B_INT8>(pl.bm, pl.bn, p, stream);
+  if (e != hipSuccess || pl.splits == 1) return e;
+  return launch_reduce(p, stream);
 }
 
 }  // namespace mj

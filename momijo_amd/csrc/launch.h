@@ -26,9 +26,21 @@ struct GemmNT {
   int64_t M = 0, N = 0, K = 0;
   int bkind = B_BF16;
   bool gate_up = false;         // C = silu(A B^T * s) * (A B2^T * s2)
+  float *part = nullptr;        // split-K partials [splits][M][N] fp32 (workspace)
+  int splits = 1;
 };
 
-hipError_t launch_gemm_nt(const GemmNT &p, hipStream_t stream);
+// Tile shape and K split chosen for a problem (the split needs a workspace of
+// splits * M * N fp32 passed as GemmNT::part).
+struct GemmPlan {
+  int bm = 256, bn = 256, splits = 1;
+  size_t workspace_bytes(const GemmNT &p) const {
+    return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
+  }
+};
+
+GemmPlan plan_gemm_nt(const GemmNT &p);
+hipError_t launch_gemm_nt(const GemmNT &p, const GemmPlan &plan, hipStream_t stream);
 
 // ---- gemm_f32.hip ---------------------------------------------------------
 hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
