@@ -88,56 +88,93 @@ __device__ __forceinline__ void store4_bf16(const GemmNT &p, int m, int nb, cons
   }
 }
 
-// Epilogue of the gen2 kernel for one activation E: scale, bias, E, bf16.
-template <int E, int TM, int TN, int WM, int WN>
-__device__ __forceinline__ void store_tile8(const GemmNT &p, const f32x16 (&acc)[TM][TN], int m0,
-                                            int n0, int wm, int wn, int lane) {
+// Output staging: after the K loop the LDS is free, so the finished bf16 tile
+// is written there (rows padded by 8 elements) and then stored to HBM row by
+// row, 16 bytes per lane: every 128-byte line of C is written by one store
+// instruction.  Writing straight from the MFMA layout would build each line
+// from 8 separate 16-byte stores, and with every workgroup in its epilogue at
+// once those lines are evicted half-written (about 5x the output bytes).
+template <int BN_OUT>
+constexpr int stage_ld() { return BN_OUT + 8; }
+
+template <int BM, int BN_OUT>
+__device__ __forceinline__ void flush_tile(const GemmNT &p, const uint16_t *ct, int m0, int n0) {
+  constexpr int LD = stage_ld<BN_OUT>();
+  constexpr int CPR = BN_OUT / 8;               // 16-byte chunks per tile row
+  constexpr int TOTAL = BM * CPR;
   const int M = (int)p.M, N = (int)p.N;
+  const bool vec = (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0;
+#pragma unroll 4
+  for (int idx = threadIdx.x; idx < TOTAL; idx += 512) {
+    const int r = idx / CPR, ch = idx % CPR;
+    const int m = m0 + r, n = n0 + ch * 8;
+    if (m >= M || n >= N) continue;
+    const uint4 v = *(const uint4 *)(ct + r * LD + ch * 8);
+    uint16_t *dst = p.C + (size_t)m * p.ldc + n;
+    if (vec && n + 7 < N) {
+      *(uint4 *)dst = v;
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (n + q < N) dst[q] = (uint16_t)(w[q >> 1] >> (16 * (q & 1)));
+    }
+  }
+}
+
+// Epilogue for one activation E: scale, bias, E, bf16 into the staging tile.
+template <int E, int TM, int TN, int WM, int WN, int BN_OUT>
+__device__ __forceinline__ void stage_tile(const GemmNT &p, const f32x16 (&acc)[TM][TN],
+                                           uint16_t *ct, int n0, int wm, int wn, int lane) {
+  constexpr int LD = stage_ld<BN_OUT>();
+  const int N = (int)p.N;
   const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int nb = n0 + wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+      const int nl = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);  // column in the tile
       float s[4], b[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = nb + q < N ? nb + q : N - 1;
+        const int n = n0 + nl + q < N ? n0 + nl + q : N - 1;
         s[q] = has_s ? p.scales[n] : 1.0f;
         b[q] = has_b ? p.bias[n] : 0.0f;
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        const int ml = wm * WM + i * 32 + (lane & 31);
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           v[q] = apply_epi(E, epi_scale_bias(acc[i][j][4 * g + q], s[q], b[q], has_s, has_b));
-        if (m < M) store4_bf16(p, m, nb, v);
+        *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(v[0], v[1]),
+                                                   pack_bf16x2(v[2], v[3]));
       }
     }
   }
 }
 
-// Gate/up epilogue: subtile 0 is the gate, subtile 1 the up projection of the
-// same output columns; h = silu32(g * sg) * (u * su).
-template <int TM, int WM, int WN>
-__device__ __forceinline__ void store_gateup8(const GemmNT &p, const f32x16 (&acc)[TM][2], int m0,
-                                              int n0, int wm, int wn, int lane) {
-  const int M = (int)p.M, N = (int)p.N;
+// Gate/up epilogue into the staging tile: subtile 0 is the gate, subtile 1
+// the up projection of the same output columns; h = silu32(g*sg) * (u*su).
+template <int TM, int WM, int WN, int BN_OUT>
+__device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x16 (&acc)[TM][2],
+                                             uint16_t *ct, int n0, int wm, int wn, int lane) {
+  constexpr int LD = stage_ld<BN_OUT>();
+  const int N = (int)p.N;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const int nb = n0 + wn * (WN / 2) + 8 * g + 4 * (lane >> 5);
+    const int nl = wn * (WN / 2) + 8 * g + 4 * (lane >> 5);
     float sg[4], su[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = nb + q < N ? nb + q : N - 1;
+      const int n = n0 + nl + q < N ? n0 + nl + q : N - 1;
       sg[q] = p.scales[n];
       su[q] = p.scales2[n];
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm * WM + i * 32 + (lane & 31);
+      const int ml = wm * WM + i * 32 + (lane & 31);
       float h[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -148,7 +185,7 @@ __device__ __forceinline__ void store_gateup8(const GemmNT &p, const f32x16 (&ac
           h[q] = silu32(gv) * uv;
         }
       }
-      if (m < M) store4_bf16(p, m, nb, h);
+      *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
     }
   }
 }
@@ -363,23 +400,25 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
     if constexpr (!GATEUP) store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, split);
     return;
   }
+  // every wave has left the K loop (its last barrier), so the LDS is free
+  uint16_t *ct = lds;
   if constexpr (!GATEUP) {
     switch (p.epi) {
-      case EPI_RELU: store_tile8<EPI_RELU, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      case EPI_GELU_TANH:
-        store_tile8<EPI_GELU_TANH, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      case EPI_SILU: store_tile8<EPI_SILU, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      case EPI_GELU_TANH_APPROX:
-        store_tile8<EPI_GELU_TANH_APPROX, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      case EPI_SILU_APPROX:
-        store_tile8<EPI_SILU_APPROX, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      case EPI_RELU_UNARY:
-        store_tile8<EPI_RELU_UNARY, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
-      default: store_tile8<EPI_NONE, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+#define MJ_STAGE(E) stage_tile<E, TM, TN, WM, WN, BN_OUT>(p, acc, ct, n0, wm, wn, lane); break;
+      case EPI_RELU: MJ_STAGE(EPI_RELU)
+      case EPI_GELU_TANH: MJ_STAGE(EPI_GELU_TANH)
+      case EPI_SILU: MJ_STAGE(EPI_SILU)
+      case EPI_GELU_TANH_APPROX: MJ_STAGE(EPI_GELU_TANH_APPROX)
+      case EPI_SILU_APPROX: MJ_STAGE(EPI_SILU_APPROX)
+      case EPI_RELU_UNARY: MJ_STAGE(EPI_RELU_UNARY)
+      default: MJ_STAGE(EPI_NONE)
+#undef MJ_STAGE
     }
   } else {
-    store_gateup8<TM, WM, WN>(p, acc, m0, n0, wm, wn, lane);
+    stage_gateup<TM, WM, WN, BN_OUT>(p, acc, ct, n0, wm, wn, lane);
   }
+  __syncthreads();
+  flush_tile<BM, BN_OUT>(p, ct, m0, n0);
 }
 
 // Sums the split-K partials in split order and applies scale, bias, the
@@ -431,7 +470,11 @@ static hipError_t launch_reduce(const GemmNT &p, hipStream_t stream) {
 
 template <int BM, int BN, int BKIND, bool GATEUP>
 static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
-  constexpr size_t lds = size_t(2) * (BM + BN) * kBK * sizeof(uint16_t);
+  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
+  constexpr size_t lds_loop = size_t(2) * (BM + BN) * kBK * sizeof(uint16_t);
+  constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
+  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  static_assert(lds <= 160 * 1024, "LDS budget");
   auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -440,7 +483,6 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   const int tiles = (int)((p.M + BM - 1) / BM) * (int)((p.N + BN_OUT - 1) / BN_OUT);
   hipLaunchKernelGGL(kern, dim3(tiles * p.splits), dim3(512), lds, stream, p);
   return hipGetLastError();
