@@ -37,6 +37,17 @@ PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 matrix
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
+def _traffic(name: str):
+    """HBM bytes per launch of a kernel as measured by rocprofv3 counters
+    (FETCH_SIZE x2.0 + WRITE_SIZE, calibrated against a copy of known size);
+    recorded in profiles/hbm_traffic.json, None where not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            return json.load(f).get(name, {}).get("bytes")
+    except (OSError, ValueError):
+        return None
+
+
 def _args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -91,7 +102,8 @@ def bench_c2(steps, warmup):
         "metric": "bf16 NT GEMM TFLOP/s at 4096^3",
         "value": tflops, "unit": "TFLOP/s", "ms_per_launch": ms,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS,
+                     "traffic": _traffic("c2_bf16_gemm_4096")},
         "flops_per_launch": flops,
     }
 
@@ -158,7 +170,7 @@ def bench_c3(steps, warmup):
         "metric": "int8 weight-only GEMV GB/s (M=1)",
         "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic("c3_int8_gemv_11008x4096")},
         "bytes_per_launch": bytes_,
         "timing": "graph replay of 64 launches rotating over 8 weight copies (> MALL)",
         "eager_ms_per_launch": eager_ms,
@@ -191,7 +203,8 @@ def bench_c3_pack(steps, warmup):
         "metric": "per-channel int8 quantize/pack GB/s",
         "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                     "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": _traffic("c3pack_quantize_rowwise_11008x4096")},
         "bytes_per_launch": bytes_,
     }
 
