@@ -90,6 +90,34 @@ int32_t mj_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t
 int32_t mj_linear_f32(const float *x, const float *W, const float *bias, int32_t epilogue,
                       float *y, int64_t N, int64_t InF, int64_t OutF, void *stream);
 
+/* fp64 C[M,N] = A @ B with strides, on v_mfma_f64_16x16x4f64.  Replaces the
+ * Float64 overloads of matmul_core_mm / matmul (tensor/broadcast.mojo:
+ * 1460-1538) and matmul2d (tensor/math.mojo:7838-7880), which autograd's
+ * matmul backward calls (tensor/autograd.mojo:1542-1555). */
+int32_t mj_matmul_f64(int64_t M, int64_t N, int64_t K,
+                      const double *A, int64_t sAm, int64_t sAk,
+                      const double *B, int64_t sBk, int64_t sBn,
+                      double *C, int64_t ldc, void *stream);
+
+/* fp64 y[M] = A[M,N] x[N].  Replaces matmul_core_vec Float64
+ * (tensor/broadcast.mojo:1397-1457). */
+int32_t mj_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
+                      const double *x, int64_t sx, double *y, void *stream);
+
+/* tensordot(A, B, axes=1) for fp32 (tensor/broadcast.mojo:1694-1900):
+ * C[b, :, :] = A[b] @ B[b] over batch_rank <= 5 broadcast batch dimensions
+ * of extent batch_shape[d]; the element strides of A's and B's batch
+ * dimensions are a_batch_strides[d], b_batch_strides[d] (0 where the operand
+ * is broadcast), and A[b], B[b] are (row stride, column stride) views as in
+ * mj_matmul_f32.  C is contiguous [batch..., M, N].  The three arrays are
+ * host memory. */
+int32_t mj_tensordot_f32(int32_t batch_rank, const int64_t *batch_shape,
+                         const int64_t *a_batch_strides, const int64_t *b_batch_strides,
+                         int64_t M, int64_t N, int64_t K,
+                         const float *A, int64_t sAm, int64_t sAk,
+                         const float *B, int64_t sBk, int64_t sBn,
+                         float *C, void *stream);
+
 /* Host-pointer seam with the signature of launch_1d_linear_fw
  * (tensor/gpu/runtime.mojo:539-631): x [N,InF], wT [InF,OutF] (the layout
  * Linear.forward_gpu builds, layers.mojo:489-497), b [OutF], y [N,OutF];

@@ -47,6 +47,10 @@ SIGNATURES = {
     "mj_stream_synchronize": (_I32, [_P]),
     "mj_matmul_f32": (_I32, [_I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64, _P]),
     "mj_matvec_f32": (_I32, [_I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "mj_matmul_f64": (_I32, [_I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "mj_matvec_f64": (_I32, [_I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "mj_tensordot_f32": (_I32, [_I32, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                _P, _P]),
     "mj_linear_f32": (_I32, [_P, _P, _P, _I32, _P, _I64, _I64, _I64, _P]),
     "mj_launch_linear_fw_h": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I32]),
     "mj_activation_f32": (_I32, [_I32, _P, _P, _I64, _P]),

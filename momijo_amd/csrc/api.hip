@@ -110,6 +110,58 @@ int32_t mj_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t
                     "matvec_f32 launch");
 }
 
+int32_t mj_matmul_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t sAm,
+                      int64_t sAk, const double *B, int64_t sBk, int64_t sBn, double *C,
+                      int64_t ldc, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
+  if (ldc < N) return fail(MJ_ERR_SHAPE, "ldc (%lld) < N (%lld)", (long long)ldc, (long long)N);
+  if (sAm < 0 || sAk < 0 || sBk < 0 || sBn < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+  return hip_status(mj::launch_gemm_f64(M, N, K, A, sAm, sAk, B, sBk, sBn, C, ldc, S(stream)),
+                    "gemm_f64 launch");
+}
+
+int32_t mj_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
+                      const double *x, int64_t sx, double *y, void *stream) {
+  if (int32_t s = check_dims(M, N, 0)) return s;
+  if (M == 0) return MJ_OK;
+  if (!y || (N > 0 && (!A || !x))) return fail(MJ_ERR_ARG, "null operand");
+  if (sAm < 0 || sAn < 0 || sx < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+  return hip_status(mj::launch_matvec_f64(M, N, A, sAm, sAn, x, sx, y, S(stream)),
+                    "matvec_f64 launch");
+}
+
+int32_t mj_tensordot_f32(int32_t batch_rank, const int64_t *batch_shape,
+                         const int64_t *a_batch_strides, const int64_t *b_batch_strides,
+                         int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                         int64_t sAk, const float *B, int64_t sBk, int64_t sBn, float *C,
+                         void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (batch_rank < 0 || batch_rank > mj::BatchDesc::kMaxRank)
+    return fail(MJ_ERR_UNSUPPORTED, "batch rank must be 0..%d", mj::BatchDesc::kMaxRank);
+  if (batch_rank > 0 && (!batch_shape || !a_batch_strides || !b_batch_strides))
+    return fail(MJ_ERR_ARG, "null batch description");
+  mj::BatchDesc bd;
+  bd.rank = batch_rank;
+  int64_t batches = 1;
+  for (int d = 0; d < batch_rank; ++d) {
+    if (batch_shape[d] < 0) return fail(MJ_ERR_ARG, "negative batch extent");
+    if (a_batch_strides[d] < 0 || b_batch_strides[d] < 0)
+      return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+    bd.shape[d] = batch_shape[d];
+    bd.a_stride[d] = a_batch_strides[d];
+    bd.b_stride[d] = b_batch_strides[d];
+    batches *= batch_shape[d];
+  }
+  if (batches == 0 || M == 0 || N == 0) return MJ_OK;
+  if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
+  if (sAm < 0 || sAk < 0 || sBk < 0 || sBn < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
+  return hip_status(mj::launch_gemm_f32_batched(M, N, K, A, sAm, sAk, B, sBk, sBn, C, bd, batches,
+                                                S(stream)),
+                    "tensordot launch");
+}
+
 int32_t mj_linear_f32(const float *x, const float *W, const float *bias, int32_t epilogue,
                       float *y, int64_t N, int64_t InF, int64_t OutF, void *stream) {
   // y = x W^T: B = W^T is the stride view (sBk = 1, sBn = InF) of W.

@@ -1,12 +1,15 @@
-// fp32 engine on gfx950: the matmul / Linear of momijo's Float32 tensor
-// engine (tensor/broadcast.mojo:1543-1684, learn/nn/layers.mojo:383-433).
+// fp32 / fp64 engine on gfx950: the matmul / Linear / tensordot of momijo's
+// Float32 and Float64 tensor engine (tensor/broadcast.mojo:1397-1900,
+// tensor/math.mojo:7838-7880, learn/nn/layers.mojo:383-433).
 //
-// gemm_f32_kernel: C = epi(A @ B + bias) on v_mfma_f32_16x16x4f32 (full fp32
-// products), 64x64 tile per 256-thread workgroup, 16-wide K stages staged
-// through LDS (k-major, padded).  Operands come as (pointer, row stride,
-// column stride), which covers the reference's zero-copy transpose views;
-// the loader walks whichever dimension has unit stride with consecutive
-// lanes so global reads stay coalesced.
+// gemm_fx_kernel<T>: C = epi(A @ B + bias) on v_mfma_f32_16x16x4f32 (T = float,
+// full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), 64x64 tile per
+// 256-thread workgroup, 16-wide K stages staged through LDS (k-major,
+// padded).  Operands come as (pointer, row stride, column stride), which
+// covers the reference's zero-copy transpose views; the loader walks
+// whichever dimension has unit stride with consecutive lanes so global reads
+// stay coalesced.  A grid dimension over broadcast batch indices serves
+// tensordot's batched paths.
 #include "common.h"
 #include "launch.h"
 
@@ -14,14 +17,53 @@ namespace mj {
 
 constexpr int kFBM = 64, kFBN = 64, kFBK = 16;
 
-__global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, const float *__restrict__ A,
-                                                       int64_t sAm, int64_t sAk,
-                                                       const float *__restrict__ B, int64_t sBk,
-                                                       int64_t sBn, const float *__restrict__ bias,
-                                                       int epi, float *__restrict__ C,
-                                                       int64_t ldc) {
-  __shared__ float As[2][kFBK][kFBM + 4];
-  __shared__ float Bs[2][kFBK][kFBN + 4];
+typedef __attribute__((__vector_size__(4 * sizeof(double)))) double f64x4;
+
+template <typename T> struct Acc;
+// Both instructions read A[i][k] from lane i + 16 k and B[k][j] from lane
+// j + 16 k.  Accumulator item r of lane l holds column l % 16 and row
+// 4 (l / 16) + r for fp32, but row 4 r + l / 16 for fp64.
+template <> struct Acc<float> {
+  typedef f32x4 V;
+  static __device__ __forceinline__ V mfma(float a, float b, V c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int lane, int r) { return 4 * (lane >> 4) + r; }
+};
+template <> struct Acc<double> {
+  typedef f64x4 V;
+  static __device__ __forceinline__ V mfma(double a, double b, V c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int lane, int r) { return 4 * r + (lane >> 4); }
+};
+
+// One (batch, 64 x 64 tile) per workgroup: C[b] = epi(A[b] @ B[b] + bias).
+// The batch index (batch0 + blockIdx.y) is decomposed over up to 5 broadcast
+// batch dimensions into element offsets of A and B; C is contiguous per batch.
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const T *__restrict__ A,
+                                                      int64_t sAm, int64_t sAk,
+                                                      const T *__restrict__ B, int64_t sBk,
+                                                      int64_t sBn, const T *__restrict__ bias,
+                                                      int epi, T *__restrict__ C, int64_t ldc,
+                                                      BatchDesc bd, int64_t batch0) {
+  __shared__ T As[2][kFBK][kFBM + 4];
+  __shared__ T Bs[2][kFBK][kFBN + 4];
+
+  {
+    const int64_t bi = batch0 + blockIdx.y;
+    int64_t b = bi, oa = 0, ob = 0;
+    for (int d = bd.rank - 1; d >= 0; --d) {
+      const int64_t i = b % bd.shape[d];
+      b /= bd.shape[d];
+      oa += i * bd.a_stride[d];
+      ob += i * bd.b_stride[d];
+    }
+    A += oa;
+    B += ob;
+    C += bi * M * ldc;
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -34,7 +76,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
   const bool a_k_fast = (sAk == 1);
   const bool b_n_fast = (sBn == 1) || (sBk != 1);
 
-  float ra[4], rb[4];
+  T ra[4], rb[4];
   auto load = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -42,7 +84,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
       if (a_k_fast) { k = tid & 15; m = (tid >> 4) + 16 * i; }
       else          { m = tid & 63; k = (tid >> 6) + 4 * i; }
       const int gm = m0 + m, gk = k0 + k;
-      ra[i] = (gm < M && gk < K) ? A[(int64_t)gm * sAm + (int64_t)gk * sAk] : 0.0f;
+      ra[i] = (gm < M && gk < K) ? A[(int64_t)gm * sAm + (int64_t)gk * sAk] : T(0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -50,7 +92,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
       if (b_n_fast) { n = tid & 63; k = (tid >> 6) + 4 * i; }
       else          { k = tid & 15; n = (tid >> 4) + 16 * i; }
       const int gn = n0 + n, gk = k0 + k;
-      rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : 0.0f;
+      rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : T(0);
     }
   };
   auto store = [&](int buf) {
@@ -70,11 +112,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
     }
   };
 
-  f32x4 acc[2][2];
+  typename Acc<T>::V acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
 
   const int nk = (K + kFBK - 1) / kFBK;
   load(0);
@@ -86,7 +130,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
     if (kt + 1 < nk) load((kt + 1) * kFBK);
 #pragma unroll
     for (int kk = 0; kk < kFBK; kk += 4) {
-      float a[2], b[2];
+      T a[2], b[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) a[i] = As[buf][kk + fk][wm * 32 + i * 16 + fr];
 #pragma unroll
@@ -94,64 +138,103 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int M, int N, int K, cons
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = Acc<T>::mfma(a[i], b[j], acc[i][j]);
     }
     if (kt + 1 < nk) store(buf ^ 1);
     __syncthreads();
   }
 
-  // 16x16 output layout: lane l holds rows 4*(l/16) + r, column l%16.
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + wn * 32 + j * 16 + (lane & 15);
     if (n >= N) continue;
-    const float bb = bias ? bias[n] : 0.0f;
+    const T bb = bias ? bias[n] : T(0);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+        const int m = m0 + wm * 32 + i * 16 + Acc<T>::row(lane, r);
         if (m < M) {
-          float v = acc[i][j][r];
+          T v = acc[i][j][r];
           if (bias) {
 #pragma clang fp contract(off)
             v = v + bb;
           }
-          C[(int64_t)m * ldc + n] = apply_epi(epi, v);
+          if constexpr (sizeof(T) == sizeof(float)) v = apply_epi(epi, v);  // fp64: none
+          C[(int64_t)m * ldc + n] = v;
         }
       }
   }
+}
+
+template <typename T>
+static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t sAm,
+                            int64_t sAk, const T *B, int64_t sBk, int64_t sBn, const T *bias,
+                            int epi, T *C, int64_t ldc, const BatchDesc &bd, int64_t batches,
+                            hipStream_t stream) {
+  const int tiles = (int)((M + kFBM - 1) / kFBM) * (int)((N + kFBN - 1) / kFBN);
+  constexpr int64_t kMaxGridY = 65535;
+  for (int64_t b0 = 0; b0 < batches; b0 += kMaxGridY) {
+    const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;
+    hipLaunchKernelGGL(gemm_fx_kernel<T>, dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
+                       (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, C, ldc, bd,
+                       b0);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
                            int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                            const float *bias, int epi, float *C, int64_t ldc,
                            hipStream_t stream) {
-  const int tiles = (int)((M + kFBM - 1) / kFBM) * (int)((N + kFBN - 1) / kFBN);
-  hipLaunchKernelGGL(gemm_f32_kernel, dim3(tiles), dim3(256), 0, stream, (int)M, (int)N, (int)K,
-                     A, sAm, sAk, B, sBk, sBn, bias, epi, C, ldc);
-  return hipGetLastError();
+  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, bias, epi, C, ldc, BatchDesc{}, 1,
+                          stream);
+}
+
+hipError_t launch_gemm_f32_batched(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                                   int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
+                                   float *C, const BatchDesc &bd, int64_t batches,
+                                   hipStream_t stream) {
+  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, C, N, bd, batches,
+                          stream);
+}
+
+hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t sAm,
+                           int64_t sAk, const double *B, int64_t sBk, int64_t sBn, double *C,
+                           int64_t ldc, hipStream_t stream) {
+  return launch_fx<double>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, C, ldc, BatchDesc{}, 1,
+                           stream);
 }
 
 // y[m] = sum_n A[m,n] x[n]: one wave per row, lanes stride over n.
-__global__ __launch_bounds__(256) void matvec_f32_kernel(int M, int N, const float *__restrict__ A,
-                                                         int64_t sAm, int64_t sAn,
-                                                         const float *__restrict__ x, int64_t sx,
-                                                         float *__restrict__ y) {
+template <typename T>
+__global__ __launch_bounds__(256) void matvec_kernel(int M, int N, const T *__restrict__ A,
+                                                     int64_t sAm, int64_t sAn,
+                                                     const T *__restrict__ x, int64_t sx,
+                                                     T *__restrict__ y) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
-  const float *a = A + (int64_t)row * sAm;
-  float acc = 0.0f;
+  const T *a = A + (int64_t)row * sAm;
+  T acc = T(0);
   for (int n = lane; n < N; n += 64) acc += a[(int64_t)n * sAn] * x[(int64_t)n * sx];
-  acc = wave_sum(acc);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (lane == 0) y[row] = acc;
 }
 
 hipError_t launch_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
                              const float *x, int64_t sx, float *y, hipStream_t stream) {
-  hipLaunchKernelGGL(matvec_f32_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(matvec_kernel<float>, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+                     (int)M, (int)N, A, sAm, sAn, x, sx, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
+                             const double *x, int64_t sx, double *y, hipStream_t stream) {
+  hipLaunchKernelGGL(matvec_kernel<double>, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
                      (int)M, (int)N, A, sAm, sAn, x, sx, y);
   return hipGetLastError();
 }

@@ -225,7 +225,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds_ds
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_dst, 16, off, 0, 0, 0);
 }
 
-template <int BM, int BN, int BKIND, bool GATEUP>
+// IGLP asks the compiler to interleave the stage's MFMAs with its LDS reads
+// and buffer loads (iglp_opt 0) instead of issuing them in source order.
+template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP>
 __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
   constexpr int WGM = 2, WGN = 4;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -390,6 +392,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
                                                               acc[i][j], 0, 0, 0);
     }
     if constexpr (B_REG > 0) store_int8(buf ^ 1);
+    if constexpr (IGLP) __builtin_amdgcn_iglp_opt(0);
     // the direct loads of stage kt+1 must have landed in LDS before anyone
     // reads them: wait for this wave's loads, then the barrier covers all
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -468,14 +471,14 @@ static hipError_t launch_reduce(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BKIND, bool GATEUP>
+template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP>
 static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr size_t lds_loop = size_t(2) * (BM + BN) * kBK * sizeof(uint16_t);
   constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
   constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP>;
+  auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP, IGLP>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -488,61 +491,93 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BKIND>
+template <int BKIND, bool IGLP>
 static hipError_t launch_plain(int bm, int bn, const GemmNT &p, hipStream_t stream) {
-  if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false>(p, stream);
-  if (bm == 256 && bn == 128) return launch_tile<256, 128, BKIND, false>(p, stream);
-  if (bm == 128 && bn == 256) return launch_tile<128, 256, BKIND, false>(p, stream);
-  return launch_tile<128, 128, BKIND, false>(p, stream);
+  if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false, IGLP>(p, stream);
+  if (bm == 256 && bn == 128) return launch_tile<256, 128, BKIND, false, IGLP>(p, stream);
+  if (bm == 128 && bn == 256) return launch_tile<128, 256, BKIND, false, IGLP>(p, stream);
+  return launch_tile<128, 128, BKIND, false, IGLP>(p, stream);
 }
 
-// Chooses the tile shape and K split.  Model: a shape's relative MFMA
-// efficiency times the fraction of CU slots its grid keeps busy (a 128 x 128
-// tile uses 64 KB of LDS, so two workgroups share a CU; the larger tiles need
-// one CU each), divided by the cost of the split-K partial round trip
-// (8 B per output and split, mostly MALL-resident, against 2K flops per output).
-// The efficiencies are measured at the BASELINE shapes on MI355X.
+// Chooses the tile shape, K split and schedule by predicted time.
+//
+// A launch of W workgroups runs in rounds of (256 CUs x resident workgroups
+// per CU); a 128 x 128 tile needs 64 KB of LDS so two share a CU, the larger
+// tiles take one CU each.  A round costs (K stages per workgroup) x (time of
+// one 64-deep K stage at that shape and occupancy), and a K split adds the
+// fp32 partial round trip (8 B per output and split, plus the bf16 result)
+// at ~5 TB/s and one extra launch.  The per-stage times are measured on
+// MI355X at the BASELINE shapes (4096^3 bf16, 2048x4096x4096 and
+// 512x4096x11008 W8A16) with the schedule the plan selects; a 256 x 256
+// tile is never split (its short-K slices measured well below the model).
+namespace {
+struct StageCost {
+  int bm, bn, per_cu;
+  double us_full[2];  // per stage, CU holding per_cu workgroups: [bf16 B, int8 B]
+  double us_one[2];   // per stage, CU holding one workgroup
+};
+constexpr StageCost kStageCost[4] = {
+    {256, 256, 1, {2.22, 2.17}, {2.22, 2.17}},
+    {256, 128, 1, {1.31, 1.48}, {1.31, 1.48}},
+    {128, 256, 1, {1.34, 1.45}, {1.34, 1.45}},
+    {128, 128, 2, {1.24, 1.54}, {0.80, 0.88}},
+};
+constexpr int kCUs = 256;
+constexpr double kPartialBytesPerUs = 5.0e6;  // 5 TB/s
+constexpr double kLaunchUs = 3.0;
+}  // namespace
+
+// Whether the K loop is built with the compiler's MFMA interleave: measured
+// faster for every plain tile (C2 -3 %, C4 -10 %, C5 down -6 %), not for the
+// paired gate/up tiles.
+constexpr bool kIglpPlain = true;
+constexpr bool kIglpGateUp = false;
+
+static double plan_time_us(const GemmNT &p, int bm, int bn, int splits) {
+  for (const StageCost &c : kStageCost) {
+    if (c.bm != bm || c.bn != bn) continue;
+    const int kind = p.bkind == B_BF16 ? 0 : 1;
+    const int64_t tiles = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+    const int64_t wgs = tiles * splits;
+    const int64_t nk = (p.K + kBK - 1) / kBK;
+    const int64_t stages = (nk + splits - 1) / splits;
+    const bool full = c.per_cu > 1 && wgs > kCUs;
+    const int64_t slots = (int64_t)kCUs * (full ? c.per_cu : 1);
+    const int64_t rounds = (wgs + slots - 1) / slots;
+    double t = (double)rounds * (double)stages * (full ? c.us_full[kind] : c.us_one[kind]);
+    if (splits > 1)
+      t += ((double)splits * 8.0 + 2.0) * (double)p.M * (double)p.N / kPartialBytesPerUs +
+           kLaunchUs;
+    return t;
+  }
+  return 1e30;
+}
+
 GemmPlan plan_gemm_nt(const GemmNT &p) {
   GemmPlan pl;
-  auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
   if (p.gate_up) {
     // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
+    pl.iglp = kIglpGateUp;
     return pl;
   }
-  constexpr int kCUs = 256;
-  const int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-  const int per_cu[4] = {1, 1, 1, 2};
-  const double eff_bf16[4] = {1.0, 0.93, 0.95, 0.90};
-  const double eff_int8[4] = {1.0, 0.93, 0.95, 0.98};
-  const double *eff = p.bkind == B_BF16 ? eff_bf16 : eff_int8;
   const int64_t nk = (p.K + kBK - 1) / kBK;
-  double best = -1.0;
-  for (int s = 0; s < 4; ++s) {
-    const int64_t t = tiles(shapes[s][0], shapes[s][1]);
-    const int64_t cap = (int64_t)kCUs * per_cu[s];
-    auto util = [&](int64_t n) { return (double)n / (double)(((n + cap - 1) / cap) * cap); };
-    double score = eff[s] * util(t);
-    int splits = 1;
-    if (t < cap) {
-      int sk = (int)((cap + t - 1) / t);
-      while (sk > 1 && nk / sk < 8) --sk;  // keep >= 8 stages per split
-      if (sk > 1) {
-        const double s2 = eff[s] * util(t * sk) / (1.0 + (double)sk * 150.0 / (double)p.K);
-        if (s2 > score) {
-          score = s2;
-          splits = sk;
-        }
+  double best = 1e30;
+  for (const StageCost &c : kStageCost) {
+    const int max_split = (c.bm == 256 && c.bn == 256) ? 1 : 8;
+    for (int sk = 1; sk <= max_split; sk *= 2) {
+      if (sk > 1 && nk / sk < 8) break;  // keep >= 8 stages per split
+      const double t = plan_time_us(p, c.bm, c.bn, sk);
+      if (t < best * 0.999) {
+        best = t;
+        pl.bm = c.bm;
+        pl.bn = c.bn;
+        pl.splits = sk;
       }
     }
-    if (score > best) {
-      best = score;
-      pl.bm = shapes[s][0];
-      pl.bn = shapes[s][1];
-      pl.splits = splits;
-    }
   }
+  pl.iglp = kIglpPlain;
   return pl;
 }
 
@@ -552,13 +587,22 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
   if (p.gate_up) {
     p.splits = 1;
     p.part = nullptr;
-    if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true>(p, stream);
-    return launch_tile<128, 256, B_INT8, true>(p, stream);
+    if (pl.iglp) {
+      if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, true>(p, stream);
+      return launch_tile<128, 256, B_INT8, true, true>(p, stream);
+    }
+    if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
+    return launch_tile<128, 256, B_INT8, true, false>(p, stream);
   }
   if (pl.splits > 1 && p.part == nullptr) return hipErrorInvalidValue;
   if (pl.splits == 1) p.part = nullptr;
-  const hipError_t e = p.bkind == B_BF16 ? launch_plain<B_BF16>(pl.bm, pl.bn, p, stream)
-                                         : launch_plain<B_INT8>(pl.bm, pl.bn, p, stream);
+  hipError_t e;
+  if (p.bkind == B_BF16)
+    e = pl.iglp ? launch_plain<B_BF16, true>(pl.bm, pl.bn, p, stream)
+                : launch_plain<B_BF16, false>(pl.bm, pl.bn, p, stream);
+  else
+    e = pl.iglp ? launch_plain<B_INT8, true>(pl.bm, pl.bn, p, stream)
+                : launch_plain<B_INT8, false>(pl.bm, pl.bn, p, stream);
   if (e != hipSuccess || pl.splits == 1) return e;
   return launch_reduce(p, stream);
 }

@@ -34,6 +34,7 @@ struct GemmNT {
 // splits * M * N fp32 passed as GemmNT::part).
 struct GemmPlan {
   int bm = 256, bn = 256, splits = 1;
+  bool iglp = false;  // K loop built with the compiler's MFMA interleave
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
   }
@@ -43,6 +44,25 @@ GemmPlan plan_gemm_nt(const GemmNT &p);
 hipError_t launch_gemm_nt(const GemmNT &p, const GemmPlan &plan, hipStream_t stream);
 
 // ---- gemm_f32.hip ---------------------------------------------------------
+// Broadcast batch of matrices: element offsets of batch index b are
+// sum_d i_d * stride_d over the multi-index (i_0..i_{rank-1}) of b in shape.
+struct BatchDesc {
+  static constexpr int kMaxRank = 5;  // tensordot's generic path nests 5 batch loops
+  int rank = 0;
+  int64_t shape[kMaxRank] = {1, 1, 1, 1, 1};
+  int64_t a_stride[kMaxRank] = {0, 0, 0, 0, 0};
+  int64_t b_stride[kMaxRank] = {0, 0, 0, 0, 0};
+};
+
+hipError_t launch_gemm_f32_batched(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                                   int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
+                                   float *C, const BatchDesc &bd, int64_t batches,
+                                   hipStream_t stream);
+hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t sAm,
+                           int64_t sAk, const double *B, int64_t sBk, int64_t sBn, double *C,
+                           int64_t ldc, hipStream_t stream);
+hipError_t launch_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
+                             const double *x, int64_t sx, double *y, hipStream_t stream);
 hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
                            int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                            const float *bias, int epi, float *C, int64_t ldc,

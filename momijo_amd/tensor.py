@@ -13,6 +13,7 @@ CPU fallback.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Sequence
 
 import numpy as np
@@ -22,6 +23,7 @@ from . import _lib
 
 _DTYPES = {
     "float32": torch.float32,
+    "float64": torch.float64,
     "bfloat16": torch.bfloat16,
     "int8": torch.int8,
     "int32": torch.int32,
@@ -119,7 +121,7 @@ class Tensor:
     def matmul_vec(self, x: "Tensor") -> "Tensor":
         """Tensor.matmul_vec (tensor/tensor.mojo:3180-3181)."""
         if self._t.dim() != 2 or x._t.dim() != 1 or x._t.shape[0] != self._t.shape[1]:
-            return empty_f32()
+            return empty_f64() if self._t.dtype == torch.float64 else empty_f32()
         return _matvec(self, x)
 
     # ---------------------------------------------------------------- unary
@@ -162,12 +164,18 @@ def empty_f32() -> Tensor:
     return Tensor(torch.empty(0, dtype=torch.float32, device=_device()))
 
 
+def empty_f64() -> Tensor:
+    """empty_f64(): the reference's result for an unsupported Float64 matmul."""
+    return Tensor(torch.empty(0, dtype=torch.float64, device=_device()))
+
+
 def _matvec(A: Tensor, x: Tensor) -> Tensor:
     a, v = A._t, x._t
     M, N = a.shape
-    y = torch.empty(M, dtype=torch.float32, device=a.device)
-    _lib.call("mj_matvec_f32", M, N, _ptr(a), a.stride(0), a.stride(1), _ptr(v), v.stride(0),
-              _ptr(y), _stream())
+    fn = "mj_matvec_f64" if a.dtype == torch.float64 else "mj_matvec_f32"
+    y = torch.empty(M, dtype=a.dtype, device=a.device)
+    _lib.call(fn, M, N, _ptr(a), a.stride(0), a.stride(1), _ptr(v), v.stride(0), _ptr(y),
+              _stream())
     return Tensor(y)
 
 
@@ -179,14 +187,21 @@ def matmul(A: Tensor, B: Tensor) -> Tensor:
     need no copy).  bfloat16 operands run the bf16 MFMA GEMM, which takes B as
     the transpose view of a row-major [N, K] weight (x.matmul(W.transpose()))."""
     a, b = A._t, B._t
+    empty = empty_f64 if a.dtype == torch.float64 else empty_f32
     if a.dim() == 2 and b.dim() == 1:
-        if a.dtype != torch.float32 or b.shape[0] != a.shape[1]:
-            return empty_f32()
+        if a.dtype not in (torch.float32, torch.float64) or b.dtype != a.dtype \
+                or b.shape[0] != a.shape[1]:
+            return empty()
         return _matvec(A, B)
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
-        return empty_f32()
+        return empty()
     M, K = a.shape
     N = b.shape[1]
+    if a.dtype == torch.float64 and b.dtype == torch.float64:
+        c = torch.empty((M, N), dtype=torch.float64, device=a.device)
+        _lib.call("mj_matmul_f64", M, N, K, _ptr(a), a.stride(0), a.stride(1), _ptr(b),
+                  b.stride(0), b.stride(1), _ptr(c), N, _stream())
+        return Tensor(c)
     if a.dtype == torch.float32 and b.dtype == torch.float32:
         c = torch.empty((M, N), dtype=torch.float32, device=a.device)
         _lib.call("mj_matmul_f32", M, N, K, _ptr(a), a.stride(0), a.stride(1), _ptr(b),
@@ -201,6 +216,52 @@ def matmul(A: Tensor, B: Tensor) -> Tensor:
                   _lib.EPI_NONE, _ptr(c), N, _stream())
         return Tensor(c)
     raise TypeError(f"matmul of {a.dtype} and {b.dtype} is not supported")
+
+
+def matmul2d(a: Tensor, b: Tensor) -> Tensor:
+    """matmul2d (tensor/math.mojo:7838-7880): Float64 [m,k] @ [k,n]; bad ranks
+    or inner dimensions give zeros([m, n]) as the reference does.  Operands are
+    read through their strides; the reference indexes the raw buffer as if
+    row-major, which agrees for the contiguous tensors it is called with."""
+    at, bt = a._t, b._t
+    m = at.shape[0] if at.dim() == 2 else 0
+    n = bt.shape[1] if bt.dim() == 2 else 0
+    if at.dim() != 2 or bt.dim() != 2 or at.shape[1] != bt.shape[0]:
+        return Tensor(torch.zeros((m, n), dtype=torch.float64, device=at.device))
+    return matmul(Tensor(at.to(torch.float64)), Tensor(bt.to(torch.float64)))
+
+
+def tensordot(A: Tensor, B: Tensor, axes: int = 1) -> Tensor:
+    """tensordot (tensor/broadcast.mojo:1694-1900) for Float32, axes = 1:
+    A (..., M, K) with B (..., K, N) -> (batch..., M, N), the batch dimensions
+    broadcasting against each other.  Unsupported axes, ranks below 2, a K
+    mismatch or non-broadcastable batches give an empty tensor."""
+    a, b = A._t, B._t
+    if axes != 1 or a.dim() < 2 or b.dim() < 2:
+        return empty_f32()
+    M, K = a.shape[-2:]
+    Kb, N = b.shape[-2:]
+    if K != Kb:
+        return empty_f32()
+    try:
+        batch = tuple(torch.broadcast_shapes(a.shape[:-2], b.shape[:-2]))
+    except RuntimeError:
+        return empty_f32()
+    if a.dtype != torch.float32 or b.dtype != torch.float32:
+        raise TypeError("tensordot is defined for Float32 tensors")
+    if len(batch) > 5:
+        return empty_f32()   # the reference's generic path nests at most 5 batch loops
+    ae = a.expand(batch + (M, K))   # broadcast dims get stride 0
+    be = b.expand(batch + (K, N))
+    out = torch.empty(batch + (M, N), dtype=torch.float32, device=a.device)
+    r = len(batch)
+    arr = ctypes.c_int64 * max(r, 1)
+    shape = arr(*batch) if r else None
+    sa = arr(*ae.stride()[:r]) if r else None
+    sb = arr(*be.stride()[:r]) if r else None
+    _lib.call("mj_tensordot_f32", r, shape, sa, sb, M, N, K, _ptr(ae), ae.stride(-2),
+              ae.stride(-1), _ptr(be), be.stride(-2), be.stride(-1), _ptr(out), _stream())
+    return Tensor(out)
 
 
 def gemm_bf16_nt(A: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None,

@@ -100,6 +100,9 @@ def _declare(L):
         "mo_linear_w8a16": (None, [_P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64]),
         "mo_gemm_bf16_nt": (None, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64]),
         "mo_mlp_w8a16": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+        "mo_matmul_f64": (None, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64]),
+        "mo_matvec_f64": (None, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64]),
+        "mo_tensordot_f32": (None, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -178,6 +181,53 @@ def matmul_f32(A, B) -> np.ndarray:
     C = np.empty((M, N), np.float32)
     lib().mo_matmul_f32(A.ctypes.data, sA[0], sA[1], B.ctypes.data, sB[0], sB[1], _ptr(C), M, N, K)
     return C
+
+
+def matmul_f64(A, B) -> np.ndarray:
+    """tensor.matmul / matmul2d for 2-D float64 operands (views allowed)."""
+    A = np.asarray(A, np.float64)
+    B = np.asarray(B, np.float64)
+    M, K = A.shape
+    N = B.shape[1]
+    assert B.shape[0] == K
+    sA = [s // 8 for s in A.strides]
+    sB = [s // 8 for s in B.strides]
+    assert min(sA + sB) >= 0
+    C = np.empty((M, N), np.float64)
+    lib().mo_matmul_f64(A.ctypes.data, sA[0], sA[1], B.ctypes.data, sB[0], sB[1], _ptr(C), M, N, K)
+    return C
+
+
+def matvec_f64(A, x) -> np.ndarray:
+    A = np.asarray(A, np.float64)
+    x = np.asarray(x, np.float64)
+    M, N = A.shape
+    y = np.empty(M, np.float64)
+    lib().mo_matvec_f64(A.ctypes.data, A.strides[0] // 8, A.strides[1] // 8,
+                        x.ctypes.data, x.strides[0] // 8, _ptr(y), M, N)
+    return y
+
+
+def tensordot_f32(A, B) -> np.ndarray:
+    """tensordot(A, B, axes=1) for float32 arrays of rank >= 2 whose batch
+    dimensions (all but the last two) broadcast against each other."""
+    A = np.asarray(A, np.float32)
+    B = np.asarray(B, np.float32)
+    M, K = A.shape[-2:]
+    K2, N = B.shape[-2:]
+    assert K == K2
+    batch = np.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    Ab = np.broadcast_to(A, batch + (M, K))
+    Bb = np.broadcast_to(B, batch + (K, N))
+    nb = int(np.prod(batch)) if batch else 1
+    idx = np.indices(batch).reshape(len(batch), -1).T if batch else np.zeros((1, 0), np.int64)
+    a_off = np.array([sum(int(i) * s // 4 for i, s in zip(ix, Ab.strides[:-2])) for ix in idx], np.int64)
+    b_off = np.array([sum(int(i) * s // 4 for i, s in zip(ix, Bb.strides[:-2])) for ix in idx], np.int64)
+    C = np.empty((nb, M, N), np.float32)
+    lib().mo_tensordot_f32(A.ctypes.data, _ptr(a_off), Ab.strides[-2] // 4, Ab.strides[-1] // 4,
+                           B.ctypes.data, _ptr(b_off), Bb.strides[-2] // 4, Bb.strides[-1] // 4,
+                           _ptr(C), nb, M, N, K)
+    return C.reshape(batch + (M, N))
 
 
 def matvec_f32(A, x) -> np.ndarray:

@@ -28,8 +28,12 @@
  *   int8           constructed ties, the fp32-add artifact (0.49999997 -> 1),
  *                  all-zero rows, clamps; int32 GEMM exact by brute force.
  *   bf16 rounding  torch's bfloat16 cast (RNE) on random and special values.
+ *   fp64 engine    int64-exact products, identity/permutation, and the strict
+ *                  k order against a one-rounding-per-step numpy loop.
+ *   tensordot      per-batch equality with the pinned fp32 matmul, broadcast
+ *                  batches against materialised copies, int64 einsum.
  * Functions with no independent check are listed as "parity unpinned" in the
- * header of oracle/oracle.py.
+ * docstring of oracle/__init__.py.
  */
 #include <math.h>
 #include <stdint.h>
@@ -558,4 +562,49 @@ MO_API void mo_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
             y[(m - m0) * H + n] = mo_f32_to_bf16(acc * sd[n]);
         }
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp64 matmul (tensor/broadcast.mojo:1397-1538) and matmul2d               */
+/* (tensor/math.mojo:7838-7880)                                             */
+/* ------------------------------------------------------------------------ */
+
+/* matmul_core_mm f64 (broadcast.mojo:1460-1527): the f32 algorithm in fp64,
+ * strict ascending k, both the contiguous and the strided path. */
+MO_API void mo_matmul_f64(const double *A, int64_t sAm, int64_t sAk,
+                          const double *B, int64_t sBk, int64_t sBn,
+                          double *C, int64_t M, int64_t N, int64_t K) {
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc = acc + A[i * sAm + k * sAk] * B[k * sBk + j * sBn];
+            C[i * N + j] = acc;
+        }
+}
+
+/* matmul_core_vec f64 (broadcast.mojo:1397-1457). */
+MO_API void mo_matvec_f64(const double *A, int64_t sAm, int64_t sAn,
+                          const double *x, int64_t sx, double *y, int64_t M, int64_t N) {
+    for (int64_t i = 0; i < M; ++i) {
+        double acc = 0.0;
+        for (int64_t j = 0; j < N; ++j) acc = acc + A[i * sAm + j * sAn] * x[j * sx];
+        y[i] = acc;
+    }
+}
+
+/* tensordot f32, axes = 1 (broadcast.mojo:1694-1900): out[b, i, j] =
+ * sum_k A[b, i, k] * B[b, k, j] over the broadcast batch index b, strict
+ * ascending k.  The batch is given flattened: for each of nb output batches
+ * the caller passes the element offsets of its A and B matrices. */
+MO_API void mo_tensordot_f32(const float *A, const int64_t *a_off, int64_t sAm, int64_t sAk,
+                             const float *B, const int64_t *b_off, int64_t sBk, int64_t sBn,
+                             float *C, int64_t nb, int64_t M, int64_t N, int64_t K) {
+    for (int64_t b = 0; b < nb; ++b)
+        for (int64_t i = 0; i < M; ++i)
+            for (int64_t j = 0; j < N; ++j) {
+                float acc = 0.0f;
+                for (int64_t k = 0; k < K; ++k)
+                    acc = acc + A[a_off[b] + i * sAm + k * sAk] * B[b_off[b] + k * sBk + j * sBn];
+                C[(b * M + i) * N + j] = acc;
+            }
 }
