@@ -97,7 +97,7 @@ __device__ __forceinline__ void store4_bf16(const GemmNT &p, int m, int nb, cons
 template <int BN_OUT>
 constexpr int stage_ld() { return BN_OUT + 8; }
 
-template <int BM, int BN_OUT>
+template <int BM, int BN_OUT, int NT>
 __device__ __forceinline__ void flush_tile(const GemmNT &p, const uint16_t *ct, int m0, int n0) {
   constexpr int LD = stage_ld<BN_OUT>();
   constexpr int CPR = BN_OUT / 8;               // 16-byte chunks per tile row
@@ -105,7 +105,7 @@ __device__ __forceinline__ void flush_tile(const GemmNT &p, const uint16_t *ct, 
   const int M = (int)p.M, N = (int)p.N;
   const bool vec = (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0;
 #pragma unroll 4
-  for (int idx = threadIdx.x; idx < TOTAL; idx += 512) {
+  for (int idx = threadIdx.x; idx < TOTAL; idx += NT) {
     const int r = idx / CPR, ch = idx % CPR;
     const int m = m0 + r, n = n0 + ch * 8;
     if (m >= M || n >= N) continue;
@@ -227,15 +227,25 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds_ds
 
 // IGLP asks the compiler to interleave the stage's MFMAs with its LDS reads
 // and buffer loads (iglp_opt 0) instead of issuing them in source order.
-template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP>
-__global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
-  constexpr int WGM = 2, WGN = 4;
+// PF2 selects the K-loop pipeline for bf16 B.  Without it (and always for
+// int8 B) a stage has one barrier and stage kt+1 is loaded while stage kt
+// multiplies.  With it, all fragments of stage kt are read into registers
+// first and an LDS-only barrier then frees the buffer for stage kt+2, so
+// every load has a stage more to land (C2: 132 -> 125 us).
+//
+// NW is the number of waves: 8 (two per SIMD, laid out 2 x 4, each wave a
+// BM/2 x BN/4 subtile) or 4 (one per SIMD, 2 x 2, each wave BM/2 x BN/2 with
+// its accumulators in the accumulation registers).
+template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP, bool PF2, int NW = 8>
+__global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
+  constexpr int NT = NW * 64;
+  constexpr int WGM = 2, WGN = NW / 2;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
-  constexpr int A_DMA = BM / 64;                         // 1-KB loads per wave per stage
-  constexpr int B_DMA = BKIND == B_BF16 ? BN / 64 : 0;
-  constexpr int B_REG = BKIND == B_BF16 ? 0 : BN * 4 / 512;  // int8: 16-B chunks per thread
+  constexpr int A_DMA = BM / (8 * NW);                   // 1-KB loads per wave per stage
+  constexpr int B_DMA = BKIND == B_BF16 ? BN / (8 * NW) : 0;
+  constexpr int B_REG = BKIND == B_BF16 ? 0 : BN * 4 / NT;  // int8: 16-B chunks per thread
   static_assert(!GATEUP || TN == 2, "gate/up pairs one gate and one up subtile per wave");
   static_assert(A_DMA >= 1, "tile too small");
 
@@ -265,14 +275,14 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
   const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
   const int K = kt1 * kBK < (int)p.K ? kt1 * kBK : (int)p.K;
 
-  // ---- A: direct loads.  Block b = i*8 + wave covers tile rows [8b, 8b+8).
+  // ---- A: direct loads.  Block b = i*NW + wave covers tile rows [8b, 8b+8).
   const __amdgpu_buffer_rsrc_t rA = make_rsrc(p.A + (size_t)m0 * p.lda,
                                               ((int64_t)(M - m0) * p.lda) * 2);
   uint32_t a_off[A_DMA];
   int a_kc[A_DMA];  // logical chunk (of 8 bf16) this lane fetches
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
-    const int r = (i * 8 + wave) * 8 + (lane >> 3);
+    const int r = (i * NW + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     a_kc[i] = c;
     a_off[i] = (m0 + r < M) ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
@@ -298,7 +308,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
   bool b_up[B_DMA > 0 ? B_DMA : 1];
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
-    const int r = (i * 8 + wave) * 8 + (lane >> 3);
+    const int r = (i * NW + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     const int n = b_src_row(r, b_up[i]);
     b_kc[i] = c;
@@ -310,7 +320,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
   bool q_up[B_REG > 0 ? B_REG : 1];
 #pragma unroll
   for (int i = 0; i < B_REG; ++i) {
-    const int r = q_r + 128 * i;
+    const int r = q_r + (NT / 4) * i;
     const int n = b_src_row(r, q_up[i]);
     q_off[i] = n < N ? (uint32_t)((size_t)(n - n0) * p.ldb + q_c * 16) : kOobOffset;
   }
@@ -321,15 +331,15 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) {
       const bool ok = k0 + a_kc[i] * 8 < K;
-      dma16(rA, as + (i * 8 + wave) * 8 * kBK, ok ? a_off[i] + k0 * 2 : kOobOffset);
+      dma16(rA, as + (i * NW + wave) * 8 * kBK, ok ? a_off[i] + k0 * 2 : kOobOffset);
     }
     uint16_t *bs = Bs + buf * BN * kBK;
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) {
       const bool ok = k0 + b_kc[i] * 8 < K;
       const uint32_t off = ok ? b_off[i] + k0 * 2 : kOobOffset;
-      if (GATEUP && b_up[i]) dma16(rB2, bs + (i * 8 + wave) * 8 * kBK, off);
-      else dma16(rB, bs + (i * 8 + wave) * 8 * kBK, off);
+      if (GATEUP && b_up[i]) dma16(rB2, bs + (i * NW + wave) * 8 * kBK, off);
+      else dma16(rB, bs + (i * NW + wave) * 8 * kBK, off);
     }
 #pragma unroll
     for (int i = 0; i < B_REG; ++i) {
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
     uint16_t *bs = Bs + buf * BN * kBK;
 #pragma unroll
     for (int i = 0; i < B_REG; ++i) {
-      const int r = q_r + 128 * i;
+      const int r = q_r + (NT / 4) * i;
       uint4 lo, hi;
       i8x16_to_bf16x16(rq[i], lo, hi);
       *(uint4 *)(bs + r * kBK + swz(r, 2 * q_c)) = lo;
@@ -358,13 +368,58 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  const int fr = lane & 31;
+  const int fh = lane >> 5;
+  const int sw = (lane >> 1) & 7;
+
+  if constexpr (PF2) {
+    static_assert(B_REG == 0, "PF2 takes bf16 B only");
+    constexpr int NDMA = A_DMA + B_DMA;  // direct loads per lane per stage
+    static_assert(NDMA < 64, "vmcnt range");
+    constexpr int KS = kBK / 16;
+    issue_stage(kt0 * kBK, 0);
+    issue_stage((kt0 + 1) * kBK, 1);  // past K (or the slice) it reads zeros
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));  // stage kt0 landed
+    asm volatile("s_barrier" ::: "memory");
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const int buf = (kt - kt0) & 1;
+      const uint16_t *as = As + buf * BM * kBK + (wm * WM + fr) * kBK;
+      const uint16_t *bs = Bs + buf * BN * kBK + (wn * WN + fr) * kBK;
+      bf16x8 fa[KS][TM], fb[KS][TN];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int col = ((ks * 2 + fh) ^ sw) * 8;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[ks][i] = *(const bf16x8 *)(as + i * 32 * kBK + col);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[ks][j] = *(const bf16x8 *)(bs + j * 32 * kBK + col);
+      }
+      // every wave has its fragments of this buffer in registers: free it
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue_stage((kt + 2) * kBK, buf);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j],
+                                                                0, 0, 0);
+      if constexpr (IGLP) __builtin_amdgcn_iglp_opt(0);
+      __builtin_amdgcn_sched_barrier(0);
+      // stage kt+1 (issued one stage earlier) has landed in every wave
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));
+      asm volatile("s_barrier" ::: "memory");
+    }
+    // the zero-filled loads of stages kt1, kt1+1 may still be in flight: they
+    // target LDS that the epilogue reuses, so drain them first
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  } else {
   issue_stage(kt0 * kBK, 0);
   if constexpr (B_REG > 0) store_int8(0);
   __syncthreads();
 
-  const int fr = lane & 31;
-  const int fh = lane >> 5;
-  const int sw = (lane >> 1) & 7;
   for (int kt = kt0; kt < kt1; ++kt) {
     const int buf = (kt - kt0) & 1;
     // the other buffer was last read in stage kt-1, which every wave finished
@@ -398,6 +453,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
   }
+  }
 
   if (p.part != nullptr) {
     if constexpr (!GATEUP) store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, split);
@@ -421,7 +477,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmNT p) {
     stage_gateup<TM, WM, WN, BN_OUT>(p, acc, ct, n0, wm, wn, lane);
   }
   __syncthreads();
-  flush_tile<BM, BN_OUT>(p, ct, m0, n0);
+  flush_tile<BM, BN_OUT, NT>(p, ct, m0, n0);
 }
 
 // Sums the split-K partials in split order and applies scale, bias, the
@@ -471,14 +527,14 @@ static hipError_t launch_reduce(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP>
+template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP, bool PF2 = false, int NW = 8>
 static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr size_t lds_loop = size_t(2) * (BM + BN) * kBK * sizeof(uint16_t);
   constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
   constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP, IGLP>;
+  auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP, IGLP, PF2, NW>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -487,16 +543,16 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
     attr_set = true;
   }
   const int tiles = (int)((p.M + BM - 1) / BM) * (int)((p.N + BN_OUT - 1) / BN_OUT);
-  hipLaunchKernelGGL(kern, dim3(tiles * p.splits), dim3(512), lds, stream, p);
+  hipLaunchKernelGGL(kern, dim3(tiles * p.splits), dim3(NW * 64), lds, stream, p);
   return hipGetLastError();
 }
 
-template <int BKIND, bool IGLP>
+template <int BKIND, bool IGLP, bool PF2>
 static hipError_t launch_plain(int bm, int bn, const GemmNT &p, hipStream_t stream) {
-  if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false, IGLP>(p, stream);
-  if (bm == 256 && bn == 128) return launch_tile<256, 128, BKIND, false, IGLP>(p, stream);
-  if (bm == 128 && bn == 256) return launch_tile<128, 256, BKIND, false, IGLP>(p, stream);
-  return launch_tile<128, 128, BKIND, false, IGLP>(p, stream);
+  if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false, IGLP, PF2>(p, stream);
+  if (bm == 256 && bn == 128) return launch_tile<256, 128, BKIND, false, IGLP, PF2>(p, stream);
+  if (bm == 128 && bn == 256) return launch_tile<128, 256, BKIND, false, IGLP, PF2>(p, stream);
+  return launch_tile<128, 128, BKIND, false, IGLP, PF2>(p, stream);
 }
 
 // Chooses the tile shape, K split and schedule by predicted time.
@@ -517,21 +573,23 @@ struct StageCost {
   double us_one[2];   // per stage, CU holding one workgroup
 };
 constexpr StageCost kStageCost[4] = {
-    {256, 256, 1, {2.22, 2.17}, {2.22, 2.17}},
-    {256, 128, 1, {1.31, 1.48}, {1.31, 1.48}},
-    {128, 256, 1, {1.34, 1.45}, {1.34, 1.45}},
-    {128, 128, 2, {1.24, 1.54}, {0.80, 0.88}},
+    {256, 256, 1, {1.96, 2.17}, {1.96, 2.17}},
+    {256, 128, 1, {1.15, 1.48}, {1.15, 1.48}},
+    {128, 256, 1, {1.17, 1.45}, {1.17, 1.45}},
+    {128, 128, 2, {1.14, 1.54}, {0.80, 0.88}},
 };
 constexpr int kCUs = 256;
 constexpr double kPartialBytesPerUs = 5.0e6;  // 5 TB/s
 constexpr double kLaunchUs = 3.0;
 }  // namespace
 
-// Whether the K loop is built with the compiler's MFMA interleave: measured
-// faster for every plain tile (C2 -3 %, C4 -10 %, C5 down -6 %), not for the
-// paired gate/up tiles.
-constexpr bool kIglpPlain = true;
-constexpr bool kIglpGateUp = false;
+// Schedules: bf16 tiles run the distance-2 pipeline with the compiler's
+// MFMA interleave (iglp), except 128 x 128, where two resident workgroups
+// per CU already cover the loads and the one-barrier pipeline is 4 % faster;
+// int8 tiles run the one-barrier pipeline with iglp
+// (measured C4 -10 %, C5 down -6 %) except the 256 x 256 tile, whose register
+// budget the interleave exceeds; the paired gate/up tiles measured faster
+// without it.
 
 static double plan_time_us(const GemmNT &p, int bm, int bn, int splits) {
   for (const StageCost &c : kStageCost) {
@@ -559,7 +617,6 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
-    pl.iglp = kIglpGateUp;
     return pl;
   }
   const int64_t nk = (p.K + kBK - 1) / kBK;
@@ -577,7 +634,12 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
       }
     }
   }
-  pl.iglp = kIglpPlain;
+  if (p.bkind == B_BF16) {
+    pl.iglp = true;
+    pl.pf2 = !(pl.bm == 128 && pl.bn == 128);
+  } else {
+    pl.iglp = !(pl.bm == 256 && pl.bn == 256);
+  }
   return pl;
 }
 
@@ -587,22 +649,31 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
   if (p.gate_up) {
     p.splits = 1;
     p.part = nullptr;
-    if (pl.iglp) {
-      if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, true>(p, stream);
-      return launch_tile<128, 256, B_INT8, true, true>(p, stream);
-    }
+    if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
   }
   if (pl.splits > 1 && p.part == nullptr) return hipErrorInvalidValue;
   if (pl.splits == 1) p.part = nullptr;
   hipError_t e;
-  if (p.bkind == B_BF16)
-    e = pl.iglp ? launch_plain<B_BF16, true>(pl.bm, pl.bn, p, stream)
-                : launch_plain<B_BF16, false>(pl.bm, pl.bn, p, stream);
-  else
-    e = pl.iglp ? launch_plain<B_INT8, true>(pl.bm, pl.bn, p, stream)
-                : launch_plain<B_INT8, false>(pl.bm, pl.bn, p, stream);
+  if (p.bkind == B_BF16) {
+    // the bf16 schedules built: iglp with PF2 for the large tiles, iglp alone
+    // for 128 x 128
+    const bool small = pl.bm == 128 && pl.bn == 128;
+    if (!pl.iglp || pl.pf2 == small) return hipErrorInvalidValue;
+    if (small)
+      e = launch_tile<128, 128, B_BF16, false, true, false>(p, stream);
+    else if (pl.bm == 256 && pl.bn == 256)
+      e = launch_tile<256, 256, B_BF16, false, true, true>(p, stream);
+    else if (pl.bm == 256)
+      e = launch_tile<256, 128, B_BF16, false, true, true>(p, stream);
+    else
+      e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
+  } else {
+    if (pl.pf2) return hipErrorInvalidValue;
+    e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)
+                : launch_plain<B_INT8, false, false>(pl.bm, pl.bn, p, stream);
+  }
   if (e != hipSuccess || pl.splits == 1) return e;
   return launch_reduce(p, stream);
 }

@@ -56,7 +56,10 @@ def test_c2_full_4096(oracle, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 256), (100, 200, 72), (1, 8, 8), (300, 520, 1000),
-                                   (513, 257, 4096), (2048, 4096, 256)])
+                                   (513, 257, 4096), (2048, 4096, 256),
+                                   # 256 x 256 tiles on the distance-2 pipeline, ragged in
+                                   # M, N and in the last K stage
+                                   (3000, 3000, 136), (4096, 3000, 4000)])
 def test_bf16_shapes(oracle, dev, M, N, K):
     A, B = _inputs(oracle, M, N, K, seed_a=M + K, seed_b=N + 3 * K)
     C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev))
