@@ -92,7 +92,7 @@ int32_t mj_linear_f32(const float *x, const float *W, const float *bias, int32_t
 
 /* fp64 C[M,N] = A @ B with strides, on v_mfma_f64_16x16x4f64.  Replaces the
  * Float64 overloads of matmul_core_mm / matmul (tensor/broadcast.mojo:
- * 1460-1538) and matmul2d (tensor/math.mojo:7838-7880), which autograd's
+ * 1466-1538) and matmul2d (tensor/math.mojo:7838-7880), which autograd's
  * matmul backward calls (tensor/autograd.mojo:1542-1555). */
 int32_t mj_matmul_f64(int64_t M, int64_t N, int64_t K,
                       const double *A, int64_t sAm, int64_t sAk,
@@ -100,7 +100,7 @@ int32_t mj_matmul_f64(int64_t M, int64_t N, int64_t K,
                       double *C, int64_t ldc, void *stream);
 
 /* fp64 y[M] = A[M,N] x[N].  Replaces matmul_core_vec Float64
- * (tensor/broadcast.mojo:1397-1457). */
+ * (tensor/broadcast.mojo:1397-1464). */
 int32_t mj_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
                       const double *x, int64_t sx, double *y, void *stream);
 
@@ -118,6 +118,17 @@ int32_t mj_tensordot_f32(int32_t batch_rank, const int64_t *batch_shape,
                          const float *B, int64_t sBk, int64_t sBn,
                          float *C, void *stream);
 
+/* The MATMUL2D rule of the autograd tape (tensor/autograd.mojo:1542-1555)
+ * for y = A @ B, A [M,K], B [K,N], upstream gradient G [M,N], all Float64
+ * row-major device arrays:
+ *   dA [M,K] (+)= G @ B^T      dB [K,N] (+)= A^T @ G
+ * With accumulate != 0 the products are added to the existing dA / dB (the
+ * tape's grads[p] = grads[p].add(g)); otherwise they overwrite them.  The
+ * transposes are stride views; either output may be NULL. */
+int32_t mj_matmul_backward_f64(int64_t M, int64_t N, int64_t K, const double *A, const double *B,
+                               const double *G, double *dA, double *dB, int32_t accumulate,
+                               void *stream);
+
 /* Host-pointer seam with the signature of launch_1d_linear_fw
  * (tensor/gpu/runtime.mojo:539-631): x [N,InF], wT [InF,OutF] (the layout
  * Linear.forward_gpu builds, layers.mojo:489-497), b [OutF], y [N,OutF];
@@ -125,6 +136,29 @@ int32_t mj_tensordot_f32(int32_t batch_rank, const int64_t *batch_shape,
  * _kernel_linear_fw (layers.mojo:436-475) defines it.  Synchronous. */
 int32_t mj_launch_linear_fw_h(const float *x, const float *wT, const float *b, float *y,
                               int64_t N, int64_t InF, int64_t OutF, int32_t has_bias);
+
+/* Linear.backward (learn/nn/layers.mojo:519-618, 785-787) for x [N,InF],
+ * W [OutF,InF], dy [N,OutF] (device pointers, row-major):
+ *   dW[o,i] = sum_n dy[n,o] x[n,i]   (dW [OutF,InF], the layer's layout)
+ *   db[o]   = sum_n dy[n,o]          (strict ascending n for N <= 1024,
+ *                                     else ascending within row segments)
+ *   dx[n,i] = sum_o dy[n,o] W[o,i]   (dx [N,InF])
+ * dx and dW run on the fp32 MFMA engine over stride views (no transposed
+ * copies).  Any output may be NULL to skip it. */
+int32_t mj_linear_backward_f32(const float *x, const float *W, const float *dy, float *dW,
+                               float *db, float *dx, int64_t N, int64_t InF, int64_t OutF,
+                               void *stream);
+
+/* Host-pointer seams with the signatures of launch_1d_linear_bw_dx / _dw /
+ * _db (tensor/gpu/runtime.mojo:636-713, 714-832, 834-903).  Layouts follow
+ * the seam's CPU kernels _kernel_linear_bw_dx/_dw/_db (layers.mojo:624-729):
+ * w and dW are [OutF,InF].  (The seam's GPU kernels, runtime.mojo:75-119,
+ * index w and dW as [InF,OutF]; that layout is not reproduced.)  Synchronous. */
+int32_t mj_launch_linear_bw_dx_h(const float *dy, const float *w, float *dx, int64_t N,
+                                 int64_t InF, int64_t OutF);
+int32_t mj_launch_linear_bw_dw_h(const float *dy, const float *x, float *dW, int64_t N,
+                                 int64_t InF, int64_t OutF);
+int32_t mj_launch_linear_bw_db_h(const float *dy, float *db, int64_t N, int64_t OutF);
 
 /* Elementwise fp32 activation y = epi(x) over n elements (may alias).
  * Replaces Tensor.relu / silu / gelu (tensor/tensor.mojo:3848,4003,4020 ->

@@ -10,13 +10,14 @@ int8 helpers of learn/api/functional.mojo).
 from ._lib import (EPI_GELU_TANH, EPI_GELU_TANH_APPROX, EPI_NONE, EPI_RELU, EPI_RELU_UNARY,
                    EPI_SILU, EPI_SILU_APPROX, ROUND_LEGACY, ROUND_RHE, MomijoHipError)
 from .tensor import (Tensor, empty_f32, empty_f64, gemm_bf16_nt, gpu_available, matmul, matmul2d,
-                     tensordot)
+                     matmul_backward, tensordot)
 from .nn import Linear, QuantLinear, ReLU, W8Linear, W8MLP, quantize_rowwise_int8
 from .functional import (MinMaxObserver, convert, dequantize_i32_to_f32_add_bias,
                          matmul_i8_i8_to_i32, prepare, quantize_symmetric_int8)
 
 __all__ = [
-    "Tensor", "matmul", "matmul2d", "tensordot", "empty_f32", "empty_f64", "gemm_bf16_nt",
+    "Tensor", "matmul", "matmul2d", "matmul_backward", "tensordot", "empty_f32", "empty_f64",
+    "gemm_bf16_nt",
     "gpu_available",
     "Linear", "ReLU", "QuantLinear", "W8Linear", "W8MLP", "quantize_rowwise_int8",
     "quantize_symmetric_int8", "matmul_i8_i8_to_i32", "dequantize_i32_to_f32_add_bias",

@@ -53,6 +53,11 @@ SIGNATURES = {
                                 _P, _P]),
     "mj_linear_f32": (_I32, [_P, _P, _P, _I32, _P, _I64, _I64, _I64, _P]),
     "mj_launch_linear_fw_h": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I32]),
+    "mj_linear_backward_f32": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "mj_launch_linear_bw_dx_h": (_I32, [_P, _P, _P, _I64, _I64, _I64]),
+    "mj_launch_linear_bw_dw_h": (_I32, [_P, _P, _P, _I64, _I64, _I64]),
+    "mj_launch_linear_bw_db_h": (_I32, [_P, _P, _I64, _I64]),
+    "mj_matmul_backward_f64": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P]),
     "mj_activation_f32": (_I32, [_I32, _P, _P, _I64, _P]),
     "mj_gemm_bf16_nt": (_I32, [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I32, _P, _I64, _P]),
     "mj_quantize_symmetric_int8": (_I32, [_P, _I64, _F, _P, _P]),

@@ -60,6 +60,60 @@ int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
   return st;
 }
 
+// db = column sums of dy [N, OutF], with a stream-ordered workspace when the
+// rows are split into segments.
+int32_t run_colsum(const float *dy, int64_t N, int64_t OutF, float *db, hipStream_t stream) {
+  const int64_t segs = mj::colsum_segments(N, OutF);
+  float *part = nullptr;
+  if (segs > 1 &&
+      hipMallocAsync((void **)&part, (size_t)segs * (size_t)OutF * sizeof(float), stream) !=
+          hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "column-sum workspace allocation failed");
+  }
+  const int32_t st =
+      hip_status(mj::launch_colsum_f32(dy, N, OutF, db, part, segs, stream), "colsum launch");
+  if (part) (void)hipFreeAsync(part, stream);
+  return st;
+}
+
+// Device staging for the host-buffer seams: copies `n_in` host arrays in,
+// runs `body` on the device copies, copies `n_out` arrays back.
+struct HostArg {
+  const void *host;
+  void *host_out;
+  size_t bytes;
+};
+
+template <typename Body>
+int32_t with_device_copies(HostArg *args, int n, Body body) {
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) total += (args[i].bytes + 255) & ~(size_t)255;
+  char *dev = nullptr;
+  if (total && hipMalloc((void **)&dev, total) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "hipMalloc(%zu) failed", total);
+  }
+  void *d[8];
+  size_t off = 0;
+  int32_t st = MJ_OK;
+  for (int i = 0; i < n; ++i) {
+    d[i] = dev + off;
+    off += (args[i].bytes + 255) & ~(size_t)255;
+    if (!st && args[i].host && args[i].bytes)
+      st = hip_status(hipMemcpy(d[i], args[i].host, args[i].bytes, hipMemcpyHostToDevice),
+                      "copy in");
+  }
+  if (!st) st = body(d);
+  if (!st) st = hip_status(hipDeviceSynchronize(), "device run");
+  for (int i = 0; i < n && !st; ++i)
+    if (args[i].host_out && args[i].bytes)
+      st = hip_status(hipMemcpy(args[i].host_out, d[i], args[i].bytes, hipMemcpyDeviceToHost),
+                      "copy out");
+  if (dev) (void)hipFree(dev);
+  return st;
+}
+
 }  // namespace
 
 extern "C" {
@@ -118,7 +172,7 @@ int32_t mj_matmul_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t 
   if (!C || (K > 0 && (!A || !B))) return fail(MJ_ERR_ARG, "null operand");
   if (ldc < N) return fail(MJ_ERR_SHAPE, "ldc (%lld) < N (%lld)", (long long)ldc, (long long)N);
   if (sAm < 0 || sAk < 0 || sBk < 0 || sBn < 0) return fail(MJ_ERR_UNSUPPORTED, "negative stride");
-  return hip_status(mj::launch_gemm_f64(M, N, K, A, sAm, sAk, B, sBk, sBn, C, ldc, S(stream)),
+  return hip_status(mj::launch_gemm_f64(M, N, K, A, sAm, sAk, B, sBk, sBn, C, ldc, 0, S(stream)),
                     "gemm_f64 launch");
 }
 
@@ -194,6 +248,98 @@ int32_t mj_launch_linear_fw_h(const float *x, const float *wT, const float *b, f
   if (!st) st = hip_status(hipMemcpy(y, dy, by, hipMemcpyDeviceToHost), "copy y");
   (void)hipFree(dev);
   return st;
+}
+
+// ------------------------------------------------------------------ backward
+
+int32_t mj_linear_backward_f32(const float *x, const float *W, const float *dy, float *dW,
+                               float *db, float *dx, int64_t N, int64_t InF, int64_t OutF,
+                               void *stream) {
+  if (int32_t s = check_dims(N, InF, OutF)) return s;
+  const bool want_dx = dx && N > 0 && InF > 0;
+  const bool want_dW = dW && OutF > 0 && InF > 0;
+  const bool want_db = db && OutF > 0;
+  if ((want_dx || want_dW || want_db) && N > 0 && !dy) return fail(MJ_ERR_ARG, "null dy");
+  if (want_dx && OutF > 0 && !W) return fail(MJ_ERR_ARG, "null W");
+  if (want_dW && N > 0 && !x) return fail(MJ_ERR_ARG, "null x");
+  const hipStream_t st = S(stream);
+  // dx [N, InF] = dy [N, OutF] @ W [OutF, InF]
+  if (want_dx) {
+    if (int32_t e = hip_status(mj::launch_gemm_f32(N, InF, OutF, dy, OutF, 1, W, InF, 1, nullptr,
+                                                   MJ_EPI_NONE, dx, InF, st),
+                               "linear backward dx"))
+      return e;
+  }
+  // dW [OutF, InF] = dy^T @ x: A is the transposed view (row stride 1) of dy
+  if (want_dW) {
+    if (int32_t e = hip_status(mj::launch_gemm_f32(OutF, InF, N, dy, 1, OutF, x, InF, 1, nullptr,
+                                                   MJ_EPI_NONE, dW, InF, st),
+                               "linear backward dW"))
+      return e;
+  }
+  if (want_db) return run_colsum(dy, N, OutF, db, st);
+  return MJ_OK;
+}
+
+int32_t mj_launch_linear_bw_dx_h(const float *dy, const float *w, float *dx, int64_t N,
+                                 int64_t InF, int64_t OutF) {
+  if (int32_t s = check_dims(N, InF, OutF)) return s;
+  if (N == 0 || InF == 0) return MJ_OK;
+  if (!dx || (OutF > 0 && (!dy || !w))) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[3] = {{dy, nullptr, (size_t)N * OutF * 4}, {w, nullptr, (size_t)OutF * InF * 4},
+                  {nullptr, dx, (size_t)N * InF * 4}};
+  return with_device_copies(a, 3, [&](void **d) {
+    return mj_linear_backward_f32(nullptr, (const float *)d[1], (const float *)d[0], nullptr,
+                                  nullptr, (float *)d[2], N, InF, OutF, nullptr);
+  });
+}
+
+int32_t mj_launch_linear_bw_dw_h(const float *dy, const float *x, float *dW, int64_t N,
+                                 int64_t InF, int64_t OutF) {
+  if (int32_t s = check_dims(N, InF, OutF)) return s;
+  if (OutF == 0 || InF == 0) return MJ_OK;
+  if (!dW || (N > 0 && (!dy || !x))) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[3] = {{dy, nullptr, (size_t)N * OutF * 4}, {x, nullptr, (size_t)N * InF * 4},
+                  {nullptr, dW, (size_t)OutF * InF * 4}};
+  return with_device_copies(a, 3, [&](void **d) {
+    return mj_linear_backward_f32((const float *)d[1], nullptr, (const float *)d[0],
+                                  (float *)d[2], nullptr, nullptr, N, InF, OutF, nullptr);
+  });
+}
+
+int32_t mj_launch_linear_bw_db_h(const float *dy, float *db, int64_t N, int64_t OutF) {
+  if (int32_t s = check_dims(N, OutF, 0)) return s;
+  if (OutF == 0) return MJ_OK;
+  if (!db || (N > 0 && !dy)) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[2] = {{dy, nullptr, (size_t)N * OutF * 4}, {nullptr, db, (size_t)OutF * 4}};
+  return with_device_copies(a, 2, [&](void **d) {
+    return mj_linear_backward_f32(nullptr, nullptr, (const float *)d[0], nullptr, (float *)d[1],
+                                  nullptr, N, 1, OutF, nullptr);
+  });
+}
+
+int32_t mj_matmul_backward_f64(int64_t M, int64_t N, int64_t K, const double *A, const double *B,
+                               const double *G, double *dA, double *dB, int32_t accumulate,
+                               void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  const bool want_dA = dA && M > 0 && K > 0;
+  const bool want_dB = dB && K > 0 && N > 0;
+  if ((want_dA || want_dB) && N > 0 && M > 0 && !G) return fail(MJ_ERR_ARG, "null G");
+  if (want_dA && N > 0 && !B) return fail(MJ_ERR_ARG, "null B");
+  if (want_dB && M > 0 && !A) return fail(MJ_ERR_ARG, "null A");
+  const int accum = accumulate ? 1 : 0;
+  const hipStream_t st = S(stream);
+  // dA [M, K] (+)= G [M, N] @ B^T: B^T is the view (row stride 1, column stride N) of B [K, N]
+  if (want_dA) {
+    if (int32_t e = hip_status(mj::launch_gemm_f64(M, K, N, G, N, 1, B, 1, N, dA, K, accum, st),
+                               "matmul backward dA"))
+      return e;
+  }
+  // dB [K, N] (+)= A^T @ G: A^T is the view (row stride 1, column stride K) of A [M, K]
+  if (want_dB)
+    return hip_status(mj::launch_gemm_f64(K, N, M, A, 1, K, G, N, 1, dB, N, accum, st),
+                      "matmul backward dB");
+  return MJ_OK;
 }
 
 int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream) {

@@ -38,7 +38,9 @@ template <> struct Acc<double> {
   static __device__ __forceinline__ int row(int lane, int r) { return 4 * r + (lane >> 4); }
 };
 
-// One (batch, 64 x 64 tile) per workgroup: C[b] = epi(A[b] @ B[b] + bias).
+// One (batch, 64 x 64 tile) per workgroup: C[b] = epi(A[b] @ B[b] + bias),
+// or with accum set C[b] = C[b] + A[b] @ B[b] (gradient accumulation: the old
+// value plus the finished product, one rounding).
 // The batch index (batch0 + blockIdx.y) is decomposed over up to 5 broadcast
 // batch dimensions into element offsets of A and B; C is contiguous per batch.
 template <typename T>
@@ -46,8 +48,8 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
                                                       int64_t sAm, int64_t sAk,
                                                       const T *__restrict__ B, int64_t sBk,
                                                       int64_t sBn, const T *__restrict__ bias,
-                                                      int epi, T *__restrict__ C, int64_t ldc,
-                                                      BatchDesc bd, int64_t batch0) {
+                                                      int epi, int accum, T *__restrict__ C,
+                                                      int64_t ldc, BatchDesc bd, int64_t batch0) {
   __shared__ T As[2][kFBK][kFBM + 4];
   __shared__ T Bs[2][kFBK][kFBN + 4];
 
@@ -161,7 +163,12 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
             v = v + bb;
           }
           if constexpr (sizeof(T) == sizeof(float)) v = apply_epi(epi, v);  // fp64: none
-          C[(int64_t)m * ldc + n] = v;
+          T *dst = C + (int64_t)m * ldc + n;
+          if (accum) {
+#pragma clang fp contract(off)
+            v = *dst + v;
+          }
+          *dst = v;
         }
       }
   }
@@ -170,15 +177,15 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
 template <typename T>
 static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t sAm,
                             int64_t sAk, const T *B, int64_t sBk, int64_t sBn, const T *bias,
-                            int epi, T *C, int64_t ldc, const BatchDesc &bd, int64_t batches,
-                            hipStream_t stream) {
+                            int epi, int accum, T *C, int64_t ldc, const BatchDesc &bd,
+                            int64_t batches, hipStream_t stream) {
   const int tiles = (int)((M + kFBM - 1) / kFBM) * (int)((N + kFBN - 1) / kFBN);
   constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < batches; b0 += kMaxGridY) {
     const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;
     hipLaunchKernelGGL(gemm_fx_kernel<T>, dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
-                       (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, C, ldc, bd,
-                       b0);
+                       (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C, ldc,
+                       bd, b0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -189,23 +196,86 @@ hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int6
                            int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                            const float *bias, int epi, float *C, int64_t ldc,
                            hipStream_t stream) {
-  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, bias, epi, C, ldc, BatchDesc{}, 1,
-                          stream);
+  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, bias, epi, 0, C, ldc, BatchDesc{},
+                          1, stream);
 }
 
 hipError_t launch_gemm_f32_batched(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
                                    int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                                    float *C, const BatchDesc &bd, int64_t batches,
                                    hipStream_t stream) {
-  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, C, N, bd, batches,
+  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, 0, C, N, bd, batches,
                           stream);
 }
 
 hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t sAm,
                            int64_t sAk, const double *B, int64_t sBk, int64_t sBn, double *C,
-                           int64_t ldc, hipStream_t stream) {
-  return launch_fx<double>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, C, ldc, BatchDesc{}, 1,
-                           stream);
+                           int64_t ldc, int accum, hipStream_t stream) {
+  return launch_fx<double>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, accum, C, ldc,
+                           BatchDesc{}, 1, stream);
+}
+
+// Column sums s[o] = sum_n X[n, o] of a row-major [N, OutF] matrix, in
+// ascending n within each of `segs` consecutive row segments; a second pass
+// adds the segment sums in segment order.  With segs = 1 the order is the
+// strict ascending-n order of the reference's db loop.  One thread per
+// column: consecutive lanes read consecutive columns of a row.
+__global__ __launch_bounds__(256) void colsum_seg_kernel(const float *__restrict__ X, int64_t N,
+                                                         int64_t OutF, int64_t seg_len,
+                                                         float *__restrict__ out) {
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= OutF) return;
+  const int64_t n0 = (int64_t)blockIdx.y * seg_len;
+  const int64_t n1 = n0 + seg_len < N ? n0 + seg_len : N;
+  const float *p = X + o;
+  float s = 0.0f;
+  int64_t n = n0;
+  for (; n + 8 <= n1; n += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(n + u) * OutF];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s = s + v[u];
+  }
+  for (; n < n1; ++n) s = s + p[n * OutF];
+  out[(int64_t)blockIdx.y * OutF + o] = s;
+}
+
+__global__ __launch_bounds__(256) void colsum_combine_kernel(const float *__restrict__ part,
+                                                             int64_t segs, int64_t OutF,
+                                                             float *__restrict__ out) {
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= OutF) return;
+  float s = 0.0f;
+  for (int64_t k = 0; k < segs; ++k) s = s + part[k * OutF + o];
+  out[o] = s;
+}
+
+int64_t colsum_segments(int64_t N, int64_t OutF) {
+  const int64_t col_blocks = (OutF + 255) / 256;
+  if (N <= 1024 || col_blocks >= 1024) return 1;
+  int64_t segs = (1024 + col_blocks - 1) / col_blocks;  // ~1024 workgroups in all
+  const int64_t max_segs = (N + 63) / 64;              // at least 64 rows per segment
+  if (segs > max_segs) segs = max_segs;
+  if (segs > 65535) segs = 65535;
+  return segs;
+}
+
+hipError_t launch_colsum_f32(const float *X, int64_t N, int64_t OutF, float *out, float *part,
+                             int64_t segs, hipStream_t stream) {
+  const unsigned cb = (unsigned)((OutF + 255) / 256);
+  if (segs <= 1) {
+    hipLaunchKernelGGL(colsum_seg_kernel, dim3(cb, 1), dim3(256), 0, stream, X, N, OutF, N, out);
+    return hipGetLastError();
+  }
+  const int64_t seg_len = (N + segs - 1) / segs;
+  hipLaunchKernelGGL(colsum_seg_kernel, dim3(cb, (unsigned)segs), dim3(256), 0, stream, X, N,
+                     OutF, seg_len, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(colsum_combine_kernel, dim3(cb), dim3(256), 0, stream, part, segs, OutF,
+                     out);
+  return hipGetLastError();
 }
 
 // y[m] = sum_n A[m,n] x[n]: one wave per row, lanes stride over n.

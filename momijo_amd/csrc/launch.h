@@ -61,7 +61,12 @@ hipError_t launch_gemm_f32_batched(int64_t M, int64_t N, int64_t K, const float 
                                    hipStream_t stream);
 hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int64_t sAm,
                            int64_t sAk, const double *B, int64_t sBk, int64_t sBn, double *C,
-                           int64_t ldc, hipStream_t stream);
+                           int64_t ldc, int accum, hipStream_t stream);
+// Column sums of a row-major [N, OutF] fp32 matrix; segs from colsum_segments
+// (1 = strict ascending-n order); part holds segs * OutF floats when segs > 1.
+int64_t colsum_segments(int64_t N, int64_t OutF);
+hipError_t launch_colsum_f32(const float *X, int64_t N, int64_t OutF, float *out, float *part,
+                             int64_t segs, hipStream_t stream);
 hipError_t launch_matvec_f64(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
                              const double *x, int64_t sx, double *y, hipStream_t stream);
 hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,

@@ -42,6 +42,8 @@ class Linear:
         xt = x.torch
         if xt.dim() != 2 or xt.shape[1] != self.in_features:
             return x.copy()
+        if xt.dtype != torch.float32:
+            raise TypeError("Linear takes Float32 inputs")
         xt = xt.contiguous()
         N = xt.shape[0]
         y = torch.empty((N, self.out_features), dtype=torch.float32, device=xt.device)
@@ -55,6 +57,34 @@ class Linear:
 
     forward_auto = forward
     forward_gpu = forward
+
+    def backward(self, x: Tensor, dy: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        """Linear.backward -> backward_auto (layers.mojo:519-618, 779-787).
+
+        Returns (dW [OutF, InF], db [OutF], dx [N, InF]) with dW = dy^T x,
+        db = column sums of dy, dx = dy W.  Non-2-D operands, a row-count
+        mismatch or wrong widths return zeros shaped like (weight, bias_t, x),
+        as the reference does."""
+        xt, gt = x.torch, dy.torch
+        if (xt.dim() != 2 or gt.dim() != 2 or xt.shape[0] != gt.shape[0]
+                or xt.shape[1] != self.in_features or gt.shape[1] != self.out_features):
+            return (Tensor(torch.zeros_like(self.weight.torch)),
+                    Tensor(torch.zeros_like(self.bias_t.torch)), Tensor(torch.zeros_like(xt)))
+        if xt.dtype != torch.float32 or gt.dtype != torch.float32:
+            raise TypeError("Linear takes Float32 inputs")
+        xt, gt = xt.contiguous(), gt.contiguous()
+        w = self.weight.torch.contiguous()
+        N = xt.shape[0]
+        dW = torch.empty((self.out_features, self.in_features), dtype=torch.float32,
+                         device=xt.device)
+        db = torch.empty(self.out_features, dtype=torch.float32, device=xt.device)
+        dx = torch.empty_like(xt)
+        _lib.call("mj_linear_backward_f32", _ptr(xt), _ptr(w), _ptr(gt), _ptr(dW), _ptr(db),
+                  _ptr(dx), N, self.in_features, self.out_features, _stream())
+        return Tensor(dW), Tensor(db), Tensor(dx)
+
+    backward_auto = backward
+    backward_gpu = backward
 
 
 class ReLU:

@@ -231,6 +231,31 @@ def matmul2d(a: Tensor, b: Tensor) -> Tensor:
     return matmul(Tensor(at.to(torch.float64)), Tensor(bt.to(torch.float64)))
 
 
+def matmul_backward(a: Tensor, b: Tensor, g: Tensor, grad_a: Tensor | None = None,
+                    grad_b: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """The autograd MATMUL2D rule (tensor/autograd.mojo:1542-1555) for y = a @ b
+    in Float64: returns (grad_a + g @ b^T, grad_b + a^T @ g), each sum starting
+    from zero where no gradient is given (a fresh tape slot)."""
+    at, bt, gt = (t.torch.to(torch.float64).contiguous() for t in (a, b, g))
+    M, K = at.shape
+    N = bt.shape[1]
+    if bt.shape[0] != K or tuple(gt.shape) != (M, N):
+        raise ValueError("matmul_backward: a [M,K], b [K,N], g [M,N] expected")
+    outs = []
+    for grad, shape, which in ((grad_a, (M, K), 0), (grad_b, (K, N), 1)):
+        if grad is not None:
+            o = grad.torch.to(torch.float64).contiguous().clone()
+            if tuple(o.shape) != shape:
+                raise ValueError("gradient shape mismatch")
+        else:
+            o = torch.empty(shape, dtype=torch.float64, device=at.device)
+        _lib.call("mj_matmul_backward_f64", M, N, K, _ptr(at), _ptr(bt), _ptr(gt),
+                  _ptr(o) if which == 0 else None, _ptr(o) if which == 1 else None,
+                  int(grad is not None), _stream())
+        outs.append(Tensor(o))
+    return outs[0], outs[1]
+
+
 def tensordot(A: Tensor, B: Tensor, axes: int = 1) -> Tensor:
     """tensordot (tensor/broadcast.mojo:1694-1900) for Float32, axes = 1:
     A (..., M, K) with B (..., K, N) -> (batch..., M, N), the batch dimensions

@@ -103,6 +103,8 @@ def _declare(L):
         "mo_matmul_f64": (None, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64]),
         "mo_matvec_f64": (None, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64]),
         "mo_tensordot_f32": (None, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64]),
+        "mo_linear_backward_f32": (None, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
+        "mo_matmul_backward_f64": (None, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -196,6 +198,39 @@ def matmul_f64(A, B) -> np.ndarray:
     C = np.empty((M, N), np.float64)
     lib().mo_matmul_f64(A.ctypes.data, sA[0], sA[1], B.ctypes.data, sB[0], sB[1], _ptr(C), M, N, K)
     return C
+
+
+def linear_backward_f32(x, W, dy):
+    """Linear.backward (learn/nn/layers.mojo:519-618) -> (dW, db, dx) for
+    x [N, InF], W [OutF, InF], dy [N, OutF], strict summation order."""
+    x = _c(x, np.float32)
+    W = _c(W, np.float32)
+    dy = _c(dy, np.float32)
+    N, InF = x.shape
+    OutF = W.shape[0]
+    assert W.shape == (OutF, InF) and dy.shape == (N, OutF)
+    dW = np.empty((OutF, InF), np.float32)
+    db = np.empty(OutF, np.float32)
+    dx = np.empty((N, InF), np.float32)
+    lib().mo_linear_backward_f32(_ptr(x), _ptr(W), _ptr(dy), _ptr(dW), _ptr(db), _ptr(dx),
+                                 N, InF, OutF)
+    return dW, db, dx
+
+
+def matmul_backward_f64(a, b, g, da=None, db=None):
+    """The autograd MATMUL2D rule (tensor/autograd.mojo:1542-1555): returns
+    (da + g @ b^T, db + a^T @ g); with da/db None the sums start from zero."""
+    a = _c(a, np.float64)
+    b = _c(b, np.float64)
+    g = _c(g, np.float64)
+    M, K = a.shape
+    N = b.shape[1]
+    assert b.shape == (K, N) and g.shape == (M, N)
+    acc = 1 if (da is not None or db is not None) else 0
+    oa = _c(da, np.float64).copy() if da is not None else np.zeros((M, K))
+    ob = _c(db, np.float64).copy() if db is not None else np.zeros((K, N))
+    lib().mo_matmul_backward_f64(_ptr(a), _ptr(b), _ptr(g), _ptr(oa), _ptr(ob), M, N, K, acc)
+    return oa, ob
 
 
 def matvec_f64(A, x) -> np.ndarray:

@@ -608,3 +608,60 @@ MO_API void mo_tensordot_f32(const float *A, const int64_t *a_off, int64_t sAm, 
                 C[(b * M + i) * N + j] = acc;
             }
 }
+
+/* Linear.backward_cpu_parallel (learn/nn/layers.mojo:519-618): for
+ * x [N,InF], W [OutF,InF] and dy [N,OutF],
+ *   db[o]   = sum_n dy[n,o]                     (ascending n, :545-553)
+ *   dx[n,i] = sum_o dy[n,o] * W[o,i]            (ascending o, :555-583)
+ *   dW[o,i] = sum_n dy[n,o] * x[n,i]            (ascending n, :585-611)
+ * each a single fp32 accumulator; the 8- and 4-wide unrolls keep the order.
+ * A NULL output is skipped. */
+MO_API void mo_linear_backward_f32(const float *x, const float *W, const float *dy, float *dW,
+                                   float *db, float *dx, int64_t N, int64_t InF, int64_t OutF) {
+    if (db)
+        for (int64_t o = 0; o < OutF; ++o) {
+            float s = 0.0f;
+            for (int64_t n = 0; n < N; ++n) s = s + dy[n * OutF + o];
+            db[o] = s;
+        }
+    if (dx)
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t i = 0; i < InF; ++i) {
+                float acc = 0.0f;
+                for (int64_t o = 0; o < OutF; ++o) acc = acc + dy[n * OutF + o] * W[o * InF + i];
+                dx[n * InF + i] = acc;
+            }
+    if (dW)
+        for (int64_t o = 0; o < OutF; ++o)
+            for (int64_t i = 0; i < InF; ++i) {
+                float acc = 0.0f;
+                for (int64_t n = 0; n < N; ++n) acc = acc + dy[n * OutF + o] * x[n * InF + i];
+                dW[o * InF + i] = acc;
+            }
+}
+
+/* The MATMUL2D rule of the autograd tape (tensor/autograd.mojo:1542-1555) for
+ * y = a @ b with a [M,K], b [K,N] and upstream gradient g [M,N], Float64:
+ *   ga = matmul2d(g, b^T)  -> grads[a] = grads[a] + ga   (da [M,K])
+ *   gb = matmul2d(a^T, g)  -> grads[b] = grads[b] + gb   (db [K,N])
+ * matmul2d sums in ascending inner index (tensor/math.mojo:7864-7871); with
+ * accumulate = 0 the gradients are overwritten instead of added to (a fresh
+ * tape holds zeros there, which gives the same values).  A NULL output is
+ * skipped. */
+MO_API void mo_matmul_backward_f64(const double *a, const double *b, const double *g, double *da,
+                                   double *db, int64_t M, int64_t N, int64_t K, int accumulate) {
+    if (da)
+        for (int64_t i = 0; i < M; ++i)
+            for (int64_t k = 0; k < K; ++k) {
+                double acc = 0.0;
+                for (int64_t j = 0; j < N; ++j) acc = acc + g[i * N + j] * b[k * N + j];
+                da[i * K + k] = accumulate ? da[i * K + k] + acc : acc;
+            }
+    if (db)
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t j = 0; j < N; ++j) {
+                double acc = 0.0;
+                for (int64_t i = 0; i < M; ++i) acc = acc + a[i * K + k] * g[i * N + j];
+                db[k * N + j] = accumulate ? db[k * N + j] + acc : acc;
+            }
+}
