@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA
 PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 matrix
+PEAK_FP64_TFLOPS = 78.6     # MI355X fp64 matrix
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
@@ -54,8 +55,8 @@ def _args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,copy);"
-                   " copy is run only when named")
+    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,"
+                   "bwd,f64,copy); copy is run only when named")
     return p.parse_args()
 
 
@@ -271,6 +272,49 @@ def bench_c1(steps, warmup):
     }
 
 
+def bench_backward(steps, warmup):
+    """Linear.backward (dx, dW, db) in fp32: at the C1 size, and at a
+    4096-wide training shape where the fp32 MFMA engine is the bound."""
+    import momijo_amd as mj
+    out = []
+    for n in (256, 4096):
+        x = mj.Tensor(_rand_f32((n, n), 11))
+        dy = mj.Tensor(_rand_f32((n, n), 12))
+        lin = mj.Linear(n, n)
+        lin.weight.torch.copy_(_rand_f32((n, n), 13))
+        st = steps if n == 256 else max(3, steps // 20)
+        ms = _time_launches(lambda i: lin.backward(x, dy), st, max(1, warmup // 5))
+        flops = 2 * 2.0 * n ** 3  # dx and dW; db is N*OutF adds
+        tf = flops / (ms * 1e-3) / 1e12
+        out.append({
+            "name": f"linear_backward_f32_{n}",
+            "metric": f"fp32 Linear({n}->{n}).backward, N={n}: dx + dW + db TFLOP/s",
+            "value": tf, "unit": "TFLOP/s", "ms_per_step": ms,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_FP32_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf / PEAK_FP32_TFLOPS, "traffic": None},
+        })
+    return out
+
+
+def bench_f64(steps, warmup):
+    """Float64 matmul (matmul_core_mm / matmul2d) at 2048^3 on fp64 MFMA."""
+    import torch
+    import momijo_amd as mj
+    n = 2048
+    g = torch.Generator(device="cuda").manual_seed(21)
+    a = mj.Tensor(torch.randn((n, n), generator=g, device="cuda", dtype=torch.float64))
+    b = mj.Tensor(torch.randn((n, n), generator=g, device="cuda", dtype=torch.float64))
+    ms = _time_launches(lambda i: mj.matmul(a, b), max(3, steps // 10), max(1, warmup // 5))
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    return {
+        "name": "matmul_f64_2048",
+        "metric": "fp64 matmul 2048^3 TFLOP/s",
+        "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_FP64_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_FP64_TFLOPS, "traffic": None},
+    }
+
+
 def bench_copy(steps, warmup):
     """A plain device copy of known size: the calibration point for the
     rocprof FETCH_SIZE / WRITE_SIZE counters and the achievable HBM rate."""
@@ -327,11 +371,14 @@ def main():
     print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
-                    ("c5", bench_c5), ("c1", bench_c1), ("copy", bench_copy)):
+                    ("c5", bench_c5), ("c1", bench_c1), ("bwd", bench_backward),
+                    ("f64", bench_f64), ("copy", bench_copy)):
         if want(key) and (key != "copy" or "copy" in only):
-            r = fn(a.steps, a.warmup)
-            secondary.append(r)
-            print(f"# {key} done: {r['value']:.1f} {r['unit']}", file=sys.stderr, flush=True)
+            rs = fn(a.steps, a.warmup)
+            for r in rs if isinstance(rs, list) else [rs]:
+                secondary.append(r)
+                print(f"# {r['name']} done: {r['value']:.1f} {r['unit']}", file=sys.stderr,
+                      flush=True)
     torch.cuda.synchronize()
     gpu_wall = time.perf_counter() - t0
 
