@@ -246,8 +246,17 @@ __global__ __launch_bounds__(256) void colsum_combine_kernel(const float *__rest
                                                              float *__restrict__ out) {
   const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (o >= OutF) return;
+  const float *p = part + o;
   float s = 0.0f;
-  for (int64_t k = 0; k < segs; ++k) s = s + part[k * OutF + o];
+  int64_t k = 0;
+  for (; k + 8 <= segs; k += 8) {  // loads in flight together, adds in order
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(k + u) * OutF];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s = s + v[u];
+  }
+  for (; k < segs; ++k) s = s + p[k * OutF];
   out[o] = s;
 }
 
