@@ -77,8 +77,9 @@ int32_t run_colsum(const float *dy, int64_t N, int64_t OutF, float *db, hipStrea
   return st;
 }
 
-// Device staging for the host-buffer seams: copies `n_in` host arrays in,
-// runs `body` on the device copies, copies `n_out` arrays back.
+// Device staging for the host-buffer seams: one device block holds a copy of
+// each of the n arrays; those with `host` set are copied in, `body` runs on
+// the null stream, and those with `host_out` set are copied back.
 struct HostArg {
   const void *host;
   void *host_out;
@@ -87,6 +88,8 @@ struct HostArg {
 
 template <typename Body>
 int32_t with_device_copies(HostArg *args, int n, Body body) {
+  constexpr int kMaxArgs = 8;
+  if (n > kMaxArgs) return fail(MJ_ERR_ARG, "too many staged arrays");
   size_t total = 0;
   for (int i = 0; i < n; ++i) total += (args[i].bytes + 255) & ~(size_t)255;
   char *dev = nullptr;
@@ -94,7 +97,7 @@ int32_t with_device_copies(HostArg *args, int n, Body body) {
     (void)hipGetLastError();
     return fail(MJ_ERR_ALLOC, "hipMalloc(%zu) failed", total);
   }
-  void *d[8];
+  void *d[kMaxArgs];
   size_t off = 0;
   int32_t st = MJ_OK;
   for (int i = 0; i < n; ++i) {
@@ -105,7 +108,7 @@ int32_t with_device_copies(HostArg *args, int n, Body body) {
                       "copy in");
   }
   if (!st) st = body(d);
-  if (!st) st = hip_status(hipDeviceSynchronize(), "device run");
+  if (!st) st = hip_status(hipStreamSynchronize(nullptr), "device run");
   for (int i = 0; i < n && !st; ++i)
     if (args[i].host_out && args[i].bytes)
       st = hip_status(hipMemcpy(args[i].host_out, d[i], args[i].bytes, hipMemcpyDeviceToHost),
@@ -118,7 +121,7 @@ int32_t with_device_copies(HostArg *args, int n, Body body) {
 
 extern "C" {
 
-int32_t mj_version(void) { return 100; }
+int32_t mj_version(void) { return 101; }
 
 int32_t mj_device_available(void) {
   int n = 0;

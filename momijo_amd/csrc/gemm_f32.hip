@@ -179,7 +179,9 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
                             int64_t sAk, const T *B, int64_t sBk, int64_t sBn, const T *bias,
                             int epi, int accum, T *C, int64_t ldc, const BatchDesc &bd,
                             int64_t batches, hipStream_t stream) {
-  const int tiles = (int)((M + kFBM - 1) / kFBM) * (int)((N + kFBN - 1) / kFBN);
+  const int64_t tiles64 = ((M + kFBM - 1) / kFBM) * ((N + kFBN - 1) / kFBN);
+  if (tiles64 > INT32_MAX) return hipErrorInvalidValue;  // grid.x limit
+  const int tiles = (int)tiles64;
   constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < batches; b0 += kMaxGridY) {
     const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;

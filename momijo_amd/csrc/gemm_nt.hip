@@ -34,6 +34,8 @@
 //    second kernel sums the partials in split order and applies the epilogue.
 //  * workgroup ids are remapped so the 32 workgroups of one XCD form a
 //    compact block of tiles sharing that XCD's L2 (tile_coords).
+#include <atomic>
+
 #include "common.h"
 #include "launch.h"
 
@@ -535,15 +537,20 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   static_assert(lds <= 160 * 1024, "LDS budget");
   auto kern = gemm_nt_kernel<BM, BN, BKIND, GATEUP, IGLP, PF2, NW>;
-  static bool attr_set = false;
-  if (!attr_set) {
+  // the dynamic-LDS limit is raised once per device this kernel runs on
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set.fetch_or(bit, std::memory_order_release);
   }
-  const int tiles = (int)((p.M + BM - 1) / BM) * (int)((p.N + BN_OUT - 1) / BN_OUT);
-  hipLaunchKernelGGL(kern, dim3(tiles * p.splits), dim3(NW * 64), lds, stream, p);
+  const int64_t grid = ((p.M + BM - 1) / BM) * ((p.N + BN_OUT - 1) / BN_OUT) * p.splits;
+  if (grid > INT32_MAX) return hipErrorInvalidValue;  // grid.x limit
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * 64), lds, stream, p);
   return hipGetLastError();
 }
 

@@ -56,7 +56,7 @@ def test_enum_values_agree(oracle):
 
 
 def test_version_and_device_probe(lib):
-    assert lib.mj_version() == 100
+    assert lib.mj_version() == 101
     assert lib.mj_device_available() in (0, 1)
 
 
