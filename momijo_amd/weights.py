@@ -194,8 +194,10 @@ def load_w8(path: str, device=None, verify: bool = True):
         else:
             import torch
             from .nn import W8Linear
+            tdt = {np.dtype(np.int8): torch.int8, np.dtype(np.float32): torch.float32}
+
             def dev(a):  # file -> pinned staging buffer -> HBM
-                t = torch.empty(a.shape, dtype=torch.from_numpy(a[:0]).dtype, pin_memory=True)
+                t = torch.empty(a.shape, dtype=tdt[a.dtype], pin_memory=True)
                 t.numpy()[...] = a
                 return t.to(device, non_blocking=True)
             lin = W8Linear(dev(q), dev(s), None if b is None else dev(b))
