@@ -1,0 +1,113 @@
+"""Edge cases of the GEMM entry points through the C ABI: padded leading
+dimensions (the kernel must read only K of each row and write only N of each
+output row), the split-K reduce path with bias and activation, the GEMV/GEMM
+switch of the W8A16 Linear, and every epilogue.
+
+Bars as elsewhere: max|d| / max|ref| <= 2e-2 for bf16 outputs against the
+oracle; the padding columns of C must keep their sentinel bits exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+import momijo_amd as mj
+from momijo_amd import _lib
+from _util import bf16_dev, bf16_host_f32, normwise_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+SENTINEL = 0x1357  # bf16 bits written into C's padding before the call
+
+
+def _ptr(t):
+    return t.data_ptr()
+
+
+def _padded_gemm(oracle, dev, M, N, K, pad_a, pad_b, pad_c, bias, epi, seed):
+    A = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed))
+    B = oracle.f32_to_bf16(oracle.randn_f32((N, K), seed=seed + 1))
+    lda, ldb, ldc = K + pad_a, K + pad_b, N + pad_c
+    rng = np.random.default_rng(seed)
+    A_pad = rng.integers(0, 2**16, size=(M, lda), dtype=np.uint16)  # garbage in the padding
+    B_pad = rng.integers(0, 2**16, size=(N, ldb), dtype=np.uint16)
+    A_pad[:, :K] = A
+    B_pad[:, :K] = B
+    C_pad = np.full((M, ldc), SENTINEL, np.uint16)
+    a, b_, c = bf16_dev(A_pad, dev), bf16_dev(B_pad, dev), bf16_dev(C_pad, dev)
+    bt = None if bias is None else to_dev(bias, dev)
+    _lib.call("mj_gemm_bf16_nt", M, N, K, _ptr(a), lda, _ptr(b_), ldb,
+              None if bt is None else _ptr(bt), epi, _ptr(c), ldc,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got_bits = c.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.all(got_bits[:, N:] == SENTINEL), "padding columns of C were written"
+    got = bf16_host_f32(c)[:, :N]
+    rows = sorted({0, 1, M // 2, M - 1})
+    for r in rows:
+        _, ref = oracle.gemm_bf16_nt(A, B, bias, epi, rows=(r, r + 1))
+        err = np.max(np.abs(got[r] - ref[0])) / max(np.max(np.abs(ref[0])), 1e-30)
+        assert err <= BF16_TOL, f"row {r}: {err:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K,pad_c", [(300, 200, 520, 24),    # 128 x 128 tiles
+                                         (300, 200, 520, 3),     # ldc % 8 != 0: scalar stores
+                                         (3000, 2600, 136, 24),  # 256 x 256, distance-2 pipeline
+                                         (32, 512, 8192, 24)])   # split-K with the reduce kernel
+def test_bf16_padded_leading_dims(oracle, dev, M, N, K, pad_c):
+    bias = oracle.randu_f32((N,), -0.5, 0.5, seed=N)
+    _padded_gemm(oracle, dev, M, N, K, 64, 40, pad_c, bias, mj.EPI_SILU, seed=M + N)
+
+
+@pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU,
+                                 mj.EPI_GELU_TANH_APPROX, mj.EPI_SILU_APPROX,
+                                 mj.EPI_RELU_UNARY])
+def test_bf16_split_k_every_epilogue(oracle, dev, epi):
+    """The split-K reduce kernel applies scale, bias and the activation."""
+    bias = oracle.randu_f32((256,), -0.5, 0.5, seed=epi)
+    _padded_gemm(oracle, dev, 16, 256, 4096, 0, 0, 8, bias, epi, seed=100 + epi)
+
+
+def _w8(oracle, M, N, K, seed):
+    x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed))
+    W = oracle.randn_f32((N, K), std=0.02, seed=seed + 1)
+    Q, s = oracle.quantize_rowwise_rhe(W)
+    b = oracle.randu_f32((N,), -1.0 / 16, 1.0 / 16, seed=seed + 2)
+    return x, Q, s, b
+
+
+@pytest.mark.parametrize("M", [8, 9])
+@pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU,
+                                 mj.EPI_GELU_TANH_APPROX, mj.EPI_SILU_APPROX,
+                                 mj.EPI_RELU_UNARY])
+def test_w8a16_gemv_gemm_switch_every_epilogue(oracle, dev, M, epi):
+    """M = 8 is the last GEMV size, M = 9 the first MFMA GEMM size."""
+    x, Q, s, b = _w8(oracle, M, 192, 512, M * 10 + epi)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), epi)
+    y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    _, ref = oracle.linear_w8a16(x, Q, s, b, epi)
+    assert normwise_rel(y, ref) <= BF16_TOL
+
+
+def test_w8a16_split_k_bias_gelu(oracle, dev):
+    """M = 64 against K = 4096 runs the int8 GEMM with a K split, so bias and
+    GELU go through the reduce kernel."""
+    x, Q, s, b = _w8(oracle, 64, 1024, 4096, 7)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_GELU_TANH)
+    y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    _, ref = oracle.linear_w8a16(x, Q, s, b, mj.EPI_GELU_TANH)
+    assert normwise_rel(y, ref) <= BF16_TOL
+
+
+def test_unaligned_operands_are_rejected(dev):
+    """The bf16 GEMM needs 16-byte aligned operands and K % 8 == 0: anything
+    else is MJ_ERR_UNSUPPORTED, not a fault."""
+    a = torch.zeros((64, 72), dtype=torch.bfloat16, device=dev)
+    b = torch.zeros((64, 72), dtype=torch.bfloat16, device=dev)
+    c = torch.zeros((64, 64), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    st = lib.mj_gemm_bf16_nt(64, 64, 70, _ptr(a), 72, _ptr(b), 72, None, 0, _ptr(c), 64, None)
+    assert st == 3  # MJ_ERR_UNSUPPORTED: K % 8
+    st = lib.mj_gemm_bf16_nt(64, 64, 64, _ptr(a) + 2, 72, _ptr(b), 72, None, 0, _ptr(c), 64, None)
+    assert st == 3  # misaligned A
+    assert not c.any()
