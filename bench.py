@@ -330,10 +330,10 @@ def bench_copy(steps, warmup):
             "read_bytes": n * 4, "write_bytes": n * 4}
 
 
-def cpu_baseline_c2(rows: int = 128):
+def cpu_baseline_c2(rows: int = 256):
     """The oracle's strict-k fp32 dot on upcast bf16 inputs (momijo's CPU
-    engine applied to bf16 data, single thread) over `rows` rows of C2."""
-    import numpy as np
+    engine applied to bf16 data, single thread) over `rows` rows of C2
+    (about 10 s of CPU work)."""
     import oracle
     oracle.build()
     K = N = 4096
@@ -343,7 +343,6 @@ def cpu_baseline_c2(rows: int = 128):
     oracle.gemm_bf16_nt(A, B, rows=(0, rows))
     dt = time.perf_counter() - t0
     flops = 2.0 * rows * N * K
-    del np
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"C2 row slab: {rows} of 4096 rows x N=4096 x K=4096 "
                       f"({dt:.1f} s, oracle/momijo_oracle.c mo_gemm_bf16_nt, gcc -O2, 1 thread)",
