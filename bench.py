@@ -6,9 +6,13 @@ accumulation, in TFLOP/s; a "step" is one GEMM launch over inputs already
 resident in HBM.  The int8 weight-only decode GEMV (config C3, GB/s against
 the HBM roofline) and the other configs are reported under ``secondary``.
 
-Timing: ``--warmup`` untimed launches, then ``--steps`` launches bracketed by
-torch.cuda.synchronize() and HIP events recorded on the stream the kernels
-are launched on (torch's current stream, which the C ABI is handed).
+Timing: ``--warmup`` untimed launches, then further untimed launches of the
+same workload until ``--settle`` seconds of load have passed (MI355X raises
+its clock over the first tens of milliseconds of load after idle; without
+this the first ~100 launches are timed on the ramp and read 10-20 % slow),
+then ``--steps`` launches bracketed by torch.cuda.synchronize() and HIP events
+recorded on the stream the kernels are launched on (torch's current stream,
+which the C ABI is handed).
 
 The GEMV's weights (45 MB) would fit in the 256 MB MALL, so its timed loop
 rotates over enough weight copies (> 256 MB) that every launch streams its
@@ -54,19 +58,37 @@ def _args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--settle", type=float, default=0.3,
+                   help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,"
                    "bwd,f64,copy); copy is run only when named")
     return p.parse_args()
 
 
+SETTLE_S = 0.3  # set from --settle in main()
+
+
+def _settle(fn):
+    """Untimed launches of fn(i) until SETTLE_S seconds of load have passed."""
+    import torch
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def _time_launches(fn, steps: int, warmup: int):
     """Average ms per launch of fn() over `steps` launches (HIP events on the
-    current stream), after `warmup` untimed ones."""
+    current stream), after `warmup` untimed ones and the settle period."""
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    _settle(fn)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -127,6 +149,7 @@ def _graph_ms_per_launch(launch, n_in_graph: int, replays: int):
             launch(i)
     g.replay()
     torch.cuda.synchronize()
+    _settle(lambda i: g.replay())
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -361,6 +384,8 @@ def main():
         print(json.dumps({"error": "no gfx950 device or libmomijo_hip.so not built"}))
         sys.exit(1)
     torch.cuda.set_device(0)
+    global SETTLE_S
+    SETTLE_S = max(0.0, a.settle)
     only = set(filter(None, a.only.split(",")))
     want = lambda k: not only or k in only  # noqa: E731
 
@@ -393,6 +418,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": head["ms_per_launch"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",

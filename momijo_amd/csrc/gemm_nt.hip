@@ -9,7 +9,10 @@
 //  * two waves share each SIMD, so one wave's LDS / global waits are covered by
 //    the other's MFMAs; waves are laid out 2 (M) x 4 (N), each owning a
 //    (BM/2) x (BN/4) sub-tile (128 x 64 for the 256 x 256 tile) of
-//    v_mfma_f32_32x32x16_bf16 accumulators;
+//    v_mfma_f32_16x16x32_bf16 accumulators (the 16 x 16 shape moves 20 %
+//    fewer register-file bytes per flop than 32 x 32 x 16: C and D are 1 KB
+//    per 16 K flop instead of 4 KB per 32 K; at 4096^3 the kernel is power
+//    limited, so that energy is time);
 //  * K advances 64 at a time through two LDS stages; the next stage's bf16
 //    tiles go from HBM straight into LDS (buffer_load ... lds: no staging
 //    registers, no ds_write), issued before the current stage's MFMAs;
@@ -21,14 +24,15 @@
 //  * LDS rows are 64 bf16 (128 B) with an XOR swizzle (see swz) that keeps
 //    both the 1-KB direct loads and the 16-byte fragment reads free of bank
 //    conflicts;
-//  * MFMA operands are swapped (the weight tile feeds the A operand), so a
-//    lane's 16 accumulators are 4 runs of 4 consecutive output columns of one
-//    output row, stored as 8-byte runs;
+//  * MFMA operands are swapped (the weight tile feeds the A operand), so each
+//    of a lane's 16 x 16 blocks holds 4 consecutive output columns of one
+//    output row;
 //  * the epilogue (per-column weight scale, bias, activation in fp32 with no
 //    FMA contraction, RNE to bf16) is instantiated per activation;
 //  * gate/up mode (Llama FFN): each wave's B rows are WN/2 gate rows then the
-//    WN/2 up rows of the same output columns, so one lane holds g and u for
-//    the same (m, n) and writes silu32(g*sg) * (u*su) directly;
+//    WN/2 up rows of the same output columns, so block j (gate) and block
+//    j + TN/2 (up) of a lane hold g and u for the same (m, n), and the lane
+//    writes silu32(g*sg) * (u*su) directly;
 //  * split-K (when the tile grid alone cannot fill the 256 CUs): workgroup
 //    (split, tile) accumulates its K slice into an fp32 partial buffer and a
 //    second kernel sums the partials in split order and applies the epilogue.
@@ -125,48 +129,48 @@ __device__ __forceinline__ void flush_tile(const GemmNT &p, const uint16_t *ct, 
 }
 
 // Epilogue for one activation E: scale, bias, E, bf16 into the staging tile.
+// A lane's block (i, j) holds tile row wm*WM + 16i + (lane & 15) at the 4
+// columns wn*WN + 16j + 4*(lane >> 4) + q.
 template <int E, int TM, int TN, int WM, int WN, int BN_OUT>
-__device__ __forceinline__ void stage_tile(const GemmNT &p, const f32x16 (&acc)[TM][TN],
+__device__ __forceinline__ void stage_tile(const GemmNT &p, const f32x4 (&acc)[TM][TN],
                                            uint16_t *ct, int n0, int wm, int wn, int lane) {
   constexpr int LD = stage_ld<BN_OUT>();
   const int N = (int)p.N;
   const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
+    const int nl = wn * WN + j * 16 + 4 * (lane >> 4);  // column in the tile
+    float s[4], b[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int nl = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);  // column in the tile
-      float s[4], b[4];
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + nl + q < N ? n0 + nl + q : N - 1;
+      s[q] = has_s ? p.scales[n] : 1.0f;
+      b[q] = has_b ? p.bias[n] : 0.0f;
+    }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + nl + q < N ? n0 + nl + q : N - 1;
-        s[q] = has_s ? p.scales[n] : 1.0f;
-        b[q] = has_b ? p.bias[n] : 0.0f;
-      }
+    for (int i = 0; i < TM; ++i) {
+      const int ml = wm * WM + i * 16 + (lane & 15);
+      float v[4];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int ml = wm * WM + i * 32 + (lane & 31);
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[q] = apply_epi(E, epi_scale_bias(acc[i][j][4 * g + q], s[q], b[q], has_s, has_b));
-        *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(v[0], v[1]),
-                                                   pack_bf16x2(v[2], v[3]));
-      }
+      for (int q = 0; q < 4; ++q)
+        v[q] = apply_epi(E, epi_scale_bias(acc[i][j][q], s[q], b[q], has_s, has_b));
+      *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(v[0], v[1]),
+                                                 pack_bf16x2(v[2], v[3]));
     }
   }
 }
 
-// Gate/up epilogue into the staging tile: subtile 0 is the gate, subtile 1
-// the up projection of the same output columns; h = silu32(g*sg) * (u*su).
-template <int TM, int WM, int WN, int BN_OUT>
-__device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x16 (&acc)[TM][2],
+// Gate/up epilogue into the staging tile: blocks j < TN/2 are the gate,
+// blocks j + TN/2 the up projection of the same output columns;
+// h = silu32(g*sg) * (u*su).
+template <int TM, int TN, int WM, int WN, int BN_OUT>
+__device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x4 (&acc)[TM][TN],
                                              uint16_t *ct, int n0, int wm, int wn, int lane) {
   constexpr int LD = stage_ld<BN_OUT>();
   const int N = (int)p.N;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int nl = wn * (WN / 2) + 8 * g + 4 * (lane >> 5);
+  for (int j = 0; j < TN / 2; ++j) {
+    const int nl = wn * (WN / 2) + j * 16 + 4 * (lane >> 4);
     float sg[4], su[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -176,12 +180,12 @@ __device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x16 (&acc
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int ml = wm * WM + i * 32 + (lane & 31);
+      const int ml = wm * WM + i * 16 + (lane & 15);
       float h[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float gv = epi_scale_bias(acc[i][0][4 * g + q], sg[q], 0.0f, true, false);
-        const float uv = epi_scale_bias(acc[i][1][4 * g + q], su[q], 0.0f, true, false);
+        const float gv = epi_scale_bias(acc[i][j][q], sg[q], 0.0f, true, false);
+        const float uv = epi_scale_bias(acc[i][j + TN / 2][q], su[q], 0.0f, true, false);
         {
 #pragma clang fp contract(off)
           h[q] = silu32(gv) * uv;
@@ -194,31 +198,28 @@ __device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x16 (&acc
 
 // Split-K: raw fp32 sums of this workgroup's K slice, 4 columns per store.
 template <int TM, int TN, int WM, int WN>
-__device__ __forceinline__ void store_part8(const GemmNT &p, const f32x16 (&acc)[TM][TN], int m0,
+__device__ __forceinline__ void store_part8(const GemmNT &p, const f32x4 (&acc)[TM][TN], int m0,
                                             int n0, int wm, int wn, int lane, int split) {
   const int M = (int)p.M, N = (int)p.N;
   float *part = p.part + (size_t)split * M * N;
   const bool vec = (N & 3) == 0;
 #pragma unroll
-  for (int j = 0; j < TN; ++j)
+  for (int j = 0; j < TN; ++j) {
+    const int nb = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int nb = n0 + wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WM + i * 16 + (lane & 15);
+      if (m >= M) continue;
+      float *dst = part + (size_t)m * N + nb;
+      if (vec && nb + 3 < N) {
+        *(float4 *)dst = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      } else {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int m = m0 + wm * WM + i * 32 + (lane & 31);
-        if (m >= M) continue;
-        float *dst = part + (size_t)m * N + nb;
-        if (vec && nb + 3 < N) {
-          *(float4 *)dst = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1],
-                                       acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (nb + q < N) dst[q] = acc[i][j][4 * g + q];
-        }
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < N) dst[q] = acc[i][j][q];
       }
     }
+  }
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -238,17 +239,22 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds_ds
 // NW is the number of waves: 8 (two per SIMD, laid out 2 x 4, each wave a
 // BM/2 x BN/4 subtile) or 4 (one per SIMD, 2 x 2, each wave BM/2 x BN/2 with
 // its accumulators in the accumulation registers).
+//
+// Fragments of v_mfma_f32_16x16x32_bf16: lane l supplies row (l & 15) of a
+// 16-row block at the 8 consecutive K of logical chunk 4*ks + (l >> 4) of
+// the 64-deep stage (ks = 0, 1); both operands use the same chunks, so each
+// MFMA adds the products of 32 distinct K of the stage.
 template <int BM, int BN, int BKIND, bool GATEUP, bool IGLP, bool PF2, int NW = 8>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
   constexpr int NT = NW * 64;
   constexpr int WGM = 2, WGN = NW / 2;
   constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr int A_DMA = BM / (8 * NW);                   // 1-KB loads per wave per stage
   constexpr int B_DMA = BKIND == B_BF16 ? BN / (8 * NW) : 0;
   constexpr int B_REG = BKIND == B_BF16 ? 0 : BN * 4 / NT;  // int8: 16-B chunks per thread
-  static_assert(!GATEUP || TN == 2, "gate/up pairs one gate and one up subtile per wave");
+  static_assert(!GATEUP || TN == 4, "gate/up pairs two gate and two up blocks per wave");
   static_assert(A_DMA >= 1, "tile too small");
 
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -363,23 +369,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
     }
   };
 
-  f32x16 acc[TM][TN];
+  f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int fr = lane & 31;
-  const int fh = lane >> 5;
-  const int sw = (lane >> 1) & 7;
+  const int fr = lane & 15;       // row within a 16-row block
+  const int fh = lane >> 4;       // K chunk within a 32-deep MFMA step
+  const int sw = (fr >> 1) & 7;   // the row's swizzle (blocks start at multiples of 16)
+  constexpr int KS = kBK / 32;    // MFMA steps per stage
 
   if constexpr (PF2) {
     static_assert(B_REG == 0, "PF2 takes bf16 B only");
     constexpr int NDMA = A_DMA + B_DMA;  // direct loads per lane per stage
     static_assert(NDMA < 64, "vmcnt range");
-    constexpr int KS = kBK / 16;
     issue_stage(kt0 * kBK, 0);
     issue_stage((kt0 + 1) * kBK, 1);  // past K (or the slice) it reads zeros
     __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));  // stage kt0 landed
@@ -391,11 +395,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
       bf16x8 fa[KS][TM], fb[KS][TN];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int col = ((ks * 2 + fh) ^ sw) * 8;
+        const int col = ((ks * 4 + fh) ^ sw) * 8;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[ks][i] = *(const bf16x8 *)(as + i * 32 * kBK + col);
+        for (int i = 0; i < TM; ++i) fa[ks][i] = *(const bf16x8 *)(as + i * 16 * kBK + col);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fb[ks][j] = *(const bf16x8 *)(bs + j * 32 * kBK + col);
+        for (int j = 0; j < TN; ++j) fb[ks][j] = *(const bf16x8 *)(bs + j * 16 * kBK + col);
       }
       // every wave has its fragments of this buffer in registers: free it
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -406,7 +410,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j],
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], acc[i][j],
                                                                 0, 0, 0);
       if constexpr (IGLP) __builtin_amdgcn_iglp_opt(0);
       __builtin_amdgcn_sched_barrier(0);
@@ -432,21 +436,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
     const uint16_t *bs = Bs + buf * BN * kBK + (wn * WN + fr) * kBK;
     bf16x8 fa[2][TM], fb[2][TN];
     auto read_frags = [&](int slot, int ks) {
-      const int col = ((ks * 2 + fh) ^ sw) * 8;
+      const int col = ((ks * 4 + fh) ^ sw) * 8;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[slot][i] = *(const bf16x8 *)(as + i * 32 * kBK + col);
+      for (int i = 0; i < TM; ++i) fa[slot][i] = *(const bf16x8 *)(as + i * 16 * kBK + col);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[slot][j] = *(const bf16x8 *)(bs + j * 32 * kBK + col);
+      for (int j = 0; j < TN; ++j) fb[slot][j] = *(const bf16x8 *)(bs + j * 16 * kBK + col);
     };
     read_frags(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks + 1 < kBK / 16) read_frags((ks + 1) & 1, ks + 1);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_frags((ks + 1) & 1, ks + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i],
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks & 1][j], fa[ks & 1][i],
                                                               acc[i][j], 0, 0, 0);
     }
     if constexpr (B_REG > 0) store_int8(buf ^ 1);
@@ -477,7 +481,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
 #undef MJ_STAGE
     }
   } else {
-    stage_gateup<TM, WM, WN, BN_OUT>(p, acc, ct, n0, wm, wn, lane);
+    stage_gateup<TM, TN, WM, WN, BN_OUT>(p, acc, ct, n0, wm, wn, lane);
   }
   __syncthreads();
   flush_tile<BM, BN_OUT, NT>(p, ct, m0, n0);
