@@ -39,6 +39,7 @@
 //  * workgroup ids are remapped so the 32 workgroups of one XCD form a
 //    compact block of tiles sharing that XCD's L2 (tile_coords).
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "launch.h"
@@ -487,6 +488,196 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
   flush_tile<BM, BN_OUT, NT>(p, ct, m0, n0);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 x bf16 256 x 256 tiles with one wave per SIMD (4 waves, 2 x 2, each a
+// 128 x 128 subtile of 64 blocks of 16 x 16).  Against the 8-wave kernel it
+// reads a third fewer LDS bytes per flop (each wave's fragments feed 128 x 128
+// outputs instead of 128 x 64), which is what pays under the power limit.
+//
+//  * the 256 accumulator registers (64 blocks x 4) fill the accumulation
+//    register file exactly; the MFMAs are written as inline asm with the
+//    accumulator tied ("+a", D = C) so that every block stays in fixed
+//    registers (the compiler, left to itself at this pressure, rotates blocks
+//    through temporaries every iteration).  Inline asm is opaque to the hazard
+//    recognizer, so the two places where other code touches the accumulators
+//    (the zero fill before the K loop and the epilogue's reads after it) are
+//    separated from the MFMAs by explicit s_nop cover; inside the loop each
+//    block is reused only every 64 MFMAs;
+//  * K advances 64 per stage through 2 LDS buffers of 128-byte rows (the
+//    XOR swizzle of swz()); every direct load fetches 128-byte row segments,
+//    half as many L2 requests as 32-deep stages would need;
+//  * each stage is two 32-deep MFMA steps, each step 8 groups of (2 fragment
+//    reads for the next step, 8 MFMAs).  The stage's one barrier sits between
+//    its two steps: there every wave holds the stage's fragments, so the
+//    stage's buffer is free, and the direct loads of stage kt+2 go into it
+//    during the second step (2 per group); they land two steps later;
+//  * the K advance of a load is its scalar offset (no per-load VALU); the
+//    last stages, whose loads reach past K, take a per-load zero-fill select.
+//    The scalar offset stays below 2^31 and an out-of-range row offset plus it
+//    cannot wrap for K < 2^30, which the launcher checks.
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, uint16_t *lds_dst,
+                                       uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_dst, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ void mfma_16x16x32_tied(f32x4 &acc, const bf16x8 &a, const bf16x8 &b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+__global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
+  constexpr int BM = 256, BN = 256, NT = 256;
+  constexpr int WM = 128, WN = 128, TM = 8, TN = 8;
+  constexpr int DPO = 8;  // 1-KB direct loads per wave per operand per stage
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  uint16_t *As = lds;                    // [2][BM][64]
+  uint16_t *Bs = lds + 2 * BM * kBK;     // [2][BN][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  int tm, tn;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, 4, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = (K + kBK - 1) / kBK;
+
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(p.A + (size_t)m0 * p.lda,
+                                              ((int64_t)(M - m0) * p.lda) * 2);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc((const uint16_t *)p.B + (size_t)n0 * p.ldb,
+                                              ((int64_t)(N - n0) * p.ldb) * 2);
+  // 1-KB block b = i*4 + wave covers tile rows [8b, 8b+8): row 8b + lane/8,
+  // stored chunk lane%8, which holds logical chunk c of the row
+  uint32_t a_off[DPO], b_off[DPO];
+  int kc[DPO];
+#pragma unroll
+  for (int i = 0; i < DPO; ++i) {
+    const int r = (i * 4 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    kc[i] = c;
+    a_off[i] = m0 + r < M ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
+    b_off[i] = n0 + r < N ? (uint32_t)((r * p.ldb + c * 8) * 2) : kOobOffset;
+  }
+  // direct load d of stage kt into buffer buf: d < 8 is A block d, else B
+  // block d - 8.  FAST: the stage lies inside K.
+  auto load = [&](auto fast, int kt, int buf, int d) {
+    const int k0 = kt * kBK;
+    const int i = d & 7;
+    uint16_t *dst = (d < 8 ? As : Bs) + buf * BM * kBK + (i * 4 + wave) * 8 * kBK;
+    const __amdgpu_buffer_rsrc_t r = d < 8 ? rA : rB;
+    const uint32_t off = d < 8 ? a_off[i] : b_off[i];
+    if constexpr (decltype(fast)::value) {
+      dma16s(r, dst, off, (uint32_t)(k0 * 2));
+    } else {
+      const bool ok = k0 + kc[i] * 8 < K;
+      dma16s(r, dst, ok ? off + k0 * 2 : kOobOffset, 0u);
+    }
+  };
+
+  // fragment addresses of the two 32-deep steps (logical chunks 4*ks + fh)
+  const int fr = lane & 15, fh = lane >> 4;
+  const int sw = (fr >> 1) & 7;
+  const uint16_t *a_rd[2], *b_rd[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int col = ((ks * 4 + fh) ^ sw) * 8;
+    a_rd[ks] = As + (wm * WM + fr) * kBK + col;
+    b_rd[ks] = Bs + (wn * WN + fr) * kBK + col;
+  }
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8 fa[2][TM], fb[2][TN];
+
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int d = 0; d < 2 * DPO; ++d) load(std::false_type(), s, s, d);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DPO) & 0xF) | (((2 * DPO) >> 4) << 14));  // stage 0
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[0][j] = *(const bf16x8 *)(b_rd[0] + j * 16 * kBK);
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
+
+  // stage kt, held in buffer BUF (static: the loop is unrolled by two)
+  auto stage = [&](auto buf_c, auto fast, int kt) {
+    constexpr int BUF = decltype(buf_c)::value;
+    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1]
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      fa[1][j] = *(const bf16x8 *)(a_rd[1] + BUF * BM * kBK + j * 16 * kBK);
+      fb[1][j] = *(const bf16x8 *)(b_rd[1] + BUF * BN * kBK + j * 16 * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's reads of buffer BUF are done and its loads of stage kt+1
+    // have landed; after the barrier that holds for every wave
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the other buffer;
+    // load stage kt+2 into this one
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      fa[0][j] = *(const bf16x8 *)(a_rd[0] + (BUF ^ 1) * BM * kBK + j * 16 * kBK);
+      fb[0][j] = *(const bf16x8 *)(b_rd[0] + (BUF ^ 1) * BN * kBK + j * 16 * kBK);
+      load(fast, kt + 2, BUF, 2 * j);
+      load(fast, kt + 2, BUF, 2 * j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // stages kt and kt+1 load stages kt+2 and kt+3, inside K while kt+4 <= K/64
+  const int nk_full = K / kBK;
+  int kt = 0;
+  for (; kt + 4 <= nk_full; kt += 2) {
+    stage(B0(), std::true_type(), kt);
+    stage(B1(), std::true_type(), kt + 1);
+  }
+  for (; kt < nk; kt += 2) {
+    stage(B0(), std::false_type(), kt);
+    if (kt + 1 < nk) stage(B1(), std::false_type(), kt + 1);
+  }
+  // last MFMAs -> the epilogue's accumulator reads; the zero-filled loads of
+  // the two stages past the end target LDS that the epilogue reuses
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+
+  if (p.part != nullptr) {  // not planned for this tile, kept complete
+    store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, 0);
+    return;
+  }
+  uint16_t *ct = lds;
+  switch (p.epi) {
+#define MJ_STAGE(E) stage_tile<E, TM, TN, WM, WN, BN>(p, acc, ct, n0, wm, wn, lane); break;
+    case EPI_RELU: MJ_STAGE(EPI_RELU)
+    case EPI_GELU_TANH: MJ_STAGE(EPI_GELU_TANH)
+    case EPI_SILU: MJ_STAGE(EPI_SILU)
+    case EPI_GELU_TANH_APPROX: MJ_STAGE(EPI_GELU_TANH_APPROX)
+    case EPI_SILU_APPROX: MJ_STAGE(EPI_SILU_APPROX)
+    case EPI_RELU_UNARY: MJ_STAGE(EPI_RELU_UNARY)
+    default: MJ_STAGE(EPI_NONE)
+#undef MJ_STAGE
+  }
+  __syncthreads();
+  flush_tile<BM, BN, NT>(p, ct, m0, n0);
+}
+
 // Sums the split-K partials in split order and applies scale, bias, the
 // activation and the bf16 rounding; 4 columns per thread.
 template <int E>
@@ -559,6 +750,28 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+static hipError_t launch_w4(const GemmNT &p, hipStream_t stream) {
+  constexpr size_t lds_loop = size_t(2) * (256 + 256) * kBK * sizeof(uint16_t);
+  constexpr size_t lds_out = size_t(256) * stage_ld<256>() * sizeof(uint16_t);
+  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  if (p.K >= ((int64_t)1 << 30) || p.bkind != B_BF16 || p.gate_up) return hipErrorInvalidValue;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)gemm_nt_w4_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  const int64_t grid = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_nt_w4_kernel, dim3((unsigned)grid), dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
 template <int BKIND, bool IGLP, bool PF2>
 static hipError_t launch_plain(int bm, int bn, const GemmNT &p, hipStream_t stream) {
   if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false, IGLP, PF2>(p, stream);
@@ -585,7 +798,7 @@ struct StageCost {
   double us_one[2];   // per stage, CU holding one workgroup
 };
 constexpr StageCost kStageCost[4] = {
-    {256, 256, 1, {1.96, 2.17}, {1.96, 2.17}},
+    {256, 256, 1, {1.74, 2.17}, {1.74, 2.17}},  // bf16: the 4-wave kernel
     {256, 128, 1, {1.15, 1.48}, {1.15, 1.48}},
     {128, 256, 1, {1.17, 1.45}, {1.17, 1.45}},
     {128, 128, 2, {1.14, 1.54}, {0.80, 0.88}},
@@ -649,6 +862,9 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   if (p.bkind == B_BF16) {
     pl.iglp = true;
     pl.pf2 = !(pl.bm == 128 && pl.bn == 128);
+    // 256 x 256 runs the one-wave-per-SIMD kernel (its scalar K offsets need
+    // K < 2^30; beyond that the 8-wave kernel takes the tile)
+    pl.wave4 = pl.bm == 256 && pl.bn == 256 && pl.splits == 1 && p.K < ((int64_t)1 << 30);
   } else {
     pl.iglp = !(pl.bm == 256 && pl.bn == 256);
   }
@@ -672,6 +888,10 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     // the bf16 schedules built: iglp with PF2 for the large tiles, iglp alone
     // for 128 x 128
     const bool small = pl.bm == 128 && pl.bn == 128;
+    if (pl.wave4) {
+      if (pl.bm != 256 || pl.bn != 256 || pl.splits != 1) return hipErrorInvalidValue;
+      return launch_w4(p, stream);
+    }
     if (!pl.iglp || pl.pf2 == small) return hipErrorInvalidValue;
     if (small)
       e = launch_tile<128, 128, B_BF16, false, true, false>(p, stream);

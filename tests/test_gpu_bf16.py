@@ -77,6 +77,22 @@ def test_bf16_integer_inputs_bit_exact(oracle, dev):
     np.testing.assert_array_equal(bf16_host_bits(C), ref)
 
 
+@pytest.mark.parametrize("K", [320, 200])
+def test_bf16_integer_inputs_bit_exact_256_tiles(oracle, dev, K):
+    """4096 x 4096 outputs plan onto 256 x 256 tiles (the one-wave-per-SIMD
+    kernel); K = 200 ends in a partial stage.  Sums of small integers are
+    exact, so every checked row must match the oracle bit for bit."""
+    rng = np.random.default_rng(K)
+    M = N = 4096
+    Af = rng.integers(-4, 5, size=(M, K)).astype(np.float32)
+    Bf = rng.integers(-4, 5, size=(N, K)).astype(np.float32)
+    A, B = oracle.f32_to_bf16(Af), oracle.f32_to_bf16(Bf)
+    C = bf16_host_bits(mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev)))
+    for r in _rows(M):
+        ref, _ = oracle.gemm_bf16_nt(A, B, rows=(r, r + 1))
+        np.testing.assert_array_equal(C[r:r + 1], ref, err_msg=f"row {r}")
+
+
 @pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU])
 def test_bf16_bias_epilogue(oracle, dev, epi):
     M, N, K = 320, 384, 512
