@@ -520,6 +520,47 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, uint16_t *lds_d
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_dst, 16, voff, soff, 0, 0);
 }
 
+// Epilogue of a full, 16-byte aligned tile straight from the accumulators:
+// blocks j and j+1 of a lane row are exchanged with v_permlane16_swap so that
+// each lane holds 8 consecutive output columns (lane row 0: block j columns
+// 0-7, row 1: block j+1 columns 0-7, row 2: block j columns 8-15, row 3:
+// block j+1 columns 8-15) and writes them with one 16-byte store; each store
+// instruction covers 64 contiguous bytes of 16 output rows.
+template <int E, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (&acc)[TM][TN],
+                                                  int m0, int n0, int wm, int wn, int lane) {
+  const int fr = lane & 15, fh = lane >> 4;
+  const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
+#pragma unroll
+  for (int j = 0; j < TN; j += 2) {
+    float s0[4], b0[4], s1[4], b1[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int na = n0 + wn * WN + j * 16 + 4 * fh + q;
+      s0[q] = has_s ? p.scales[na] : 1.0f;
+      b0[q] = has_b ? p.bias[na] : 0.0f;
+      s1[q] = has_s ? p.scales[na + 16] : 1.0f;
+      b1[q] = has_b ? p.bias[na + 16] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float x[4], y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[q] = apply_epi(E, epi_scale_bias(acc[i][j][q], s0[q], b0[q], has_s, has_b));
+        y[q] = apply_epi(E, epi_scale_bias(acc[i][j + 1][q], s1[q], b1[q], has_s, has_b));
+      }
+      const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
+                                                       pack_bf16x2(y[0], y[1]), false, false);
+      const auto w1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[2], x[3]),
+                                                       pack_bf16x2(y[2], y[3]), false, false);
+      const int m = m0 + wm * WM + i * 16 + fr;
+      const int n = n0 + wn * WN + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
+      *(uint4 *)(p.C + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
+    }
+  }
+}
+
 __device__ __forceinline__ void mfma_16x16x32_tied(f32x4 &acc, const bf16x8 &a, const bf16x8 &b) {
   asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
@@ -662,6 +703,21 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, 0);
     return;
   }
+  if (m0 + BM <= M && n0 + BN <= N && (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0) {
+    switch (p.epi) {
+#define MJ_DIRECT(E) store_tile_direct<E, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_RELU: MJ_DIRECT(EPI_RELU)
+      case EPI_GELU_TANH: MJ_DIRECT(EPI_GELU_TANH)
+      case EPI_SILU: MJ_DIRECT(EPI_SILU)
+      case EPI_GELU_TANH_APPROX: MJ_DIRECT(EPI_GELU_TANH_APPROX)
+      case EPI_SILU_APPROX: MJ_DIRECT(EPI_SILU_APPROX)
+      case EPI_RELU_UNARY: MJ_DIRECT(EPI_RELU_UNARY)
+      default: MJ_DIRECT(EPI_NONE)
+#undef MJ_DIRECT
+    }
+    return;
+  }
+  // edge tiles and unaligned outputs: stage the tile in LDS, store row by row
   uint16_t *ct = lds;
   switch (p.epi) {
 #define MJ_STAGE(E) stage_tile<E, TM, TN, WM, WN, BN>(p, acc, ct, n0, wm, wn, lane); break;

@@ -94,8 +94,9 @@ def test_bf16_integer_inputs_bit_exact_256_tiles(oracle, dev, K):
 
 
 @pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU])
-def test_bf16_bias_epilogue(oracle, dev, epi):
-    M, N, K = 320, 384, 512
+@pytest.mark.parametrize("M,N,K", [(320, 384, 512),
+                                   (4096, 4096, 64)])  # 256 x 256 tiles, direct stores
+def test_bf16_bias_epilogue(oracle, dev, epi, M, N, K):
     A, B = _inputs(oracle, M, N, K, seed_a=31, seed_b=32)
     bias = oracle.randu_f32((N,), -1.0 / 16, 1.0 / 16, seed=5)
     C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev), to_dev(bias, dev), epi)

@@ -111,3 +111,64 @@ def test_unaligned_operands_are_rejected(dev):
     st = lib.mj_gemm_bf16_nt(64, 64, 64, _ptr(a) + 2, 72, _ptr(b), 72, None, 0, _ptr(c), 64, None)
     assert st == 3  # misaligned A
     assert not c.any()
+
+
+# fp32 bit patterns whose bf16 rounding is easy to get wrong: ties to even in
+# both directions, just below / above a tie, denormals (and a denormal tie),
+# the largest finite values (one rounds up to Inf), infinities, signed zeros
+# and quiet / signalling NaNs with payloads.
+_SPECIAL_BITS = [
+    0x3F808000, 0x3F818000, 0x3F807FFF, 0x3F808001, 0xBF808000, 0xBF818000, 0x3F80C000,
+    0x00000001, 0x00008000, 0x00018000, 0x007FFFFF, 0x80000001, 0x80018000, 0x00800000,
+    0x7F7FFFFF, 0x7F7F7FFF, 0x7F7F8000, 0xFF7FFFFF, 0x7F800000, 0xFF800000,
+    0x00000000, 0x80000000, 0x7FC00000, 0x7FC12345, 0xFFC00000, 0x7F800001, 0x7FA00000,
+    0x40490FDB, 0xC2F6E979, 0x3EAAAAAB,
+]
+
+
+def _special_bias(n, seed):
+    rng = np.random.default_rng(seed)
+    bits = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+    bits[:len(_SPECIAL_BITS)] = np.array(_SPECIAL_BITS, np.uint32)
+    return bits.view(np.float32)
+
+
+def _expected_bf16(oracle, bias):
+    # the kernels compute 0.0f + bias in fp32 and round that to bf16
+    with np.errstate(invalid="ignore"):
+        return oracle.f32_to_bf16((np.float32(0.0) + bias).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 256, 16),        # small tiles
+                                   (4096, 4096, 64)])    # 256 x 256 tiles
+def test_bf16_output_rounding_special_values(oracle, dev, M, N, K):
+    """Zero operands make every output exactly bf16(0 + bias[n]), so the bias
+    drives the kernels' fp32 -> bf16 rounding through special values; the bits
+    must equal the oracle's round-to-nearest-even conversion."""
+    bias = _special_bias(N, seed=N)
+    A = torch.zeros((M, K), dtype=torch.bfloat16, device=dev)
+    B = torch.zeros((N, K), dtype=torch.bfloat16, device=dev)
+    C = mj.gemm_bf16_nt(A, B, to_dev(bias, dev), mj.EPI_NONE)
+    got = C.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = _expected_bf16(oracle, bias)
+    bad = np.nonzero(got != want[None, :])
+    assert bad[0].size == 0, (f"{bad[0].size} mismatches, first at {bad[0][0]},{bad[1][0]}: "
+                              f"in {bias.view(np.uint32)[bad[1][0]]:#010x} "
+                              f"got {got[bad[0][0], bad[1][0]]:#06x} want {want[bad[1][0]]:#06x}")
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_w8a16_output_rounding_special_values(oracle, dev, M):
+    """The same check through the W8A16 GEMV (M = 1) and GEMM (M = 64)."""
+    N, K = 512, 256
+    bias = _special_bias(N, seed=M)
+    q = torch.zeros((N, K), dtype=torch.int8, device=dev)
+    s = torch.ones((N,), dtype=torch.float32, device=dev)
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device=dev)
+    y = mj.W8Linear(q, s, to_dev(bias, dev)).forward(x)
+    got = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = _expected_bf16(oracle, bias)
+    bad = np.nonzero(got != want[None, :])
+    assert bad[0].size == 0, (f"{bad[0].size} mismatches, first at {bad[0][0]},{bad[1][0]}: "
+                              f"in {bias.view(np.uint32)[bad[1][0]]:#010x} "
+                              f"got {got[bad[0][0], bad[1][0]]:#06x} want {want[bad[1][0]]:#06x}")
