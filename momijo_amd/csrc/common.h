@@ -156,6 +156,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// 64-lane sum without LDS traffic: two quad permutes and two row rotations
+// (DPP) leave every lane holding its 16-lane row's sum, and the four row sums
+// are read out with readlane.  Summation order: within rows pairwise by the
+// DPP pattern, then (row0 + row1) + (row2 + row3).
+#define MJ_DPP_F(v, ctrl) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false))
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += MJ_DPP_F(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += MJ_DPP_F(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += MJ_DPP_F(v, 0x124);  // row_ror:4
+  v += MJ_DPP_F(v, 0x128);  // row_ror:8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+#undef MJ_DPP_F
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -648,15 +648,20 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   // stage kt, held in buffer BUF (static: the loop is unrolled by two)
   auto stage = [&](auto buf_c, auto fast, int kt) {
     constexpr int BUF = decltype(buf_c)::value;
-    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1]
+    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1].  Each
+    // read sits between two MFMAs (sched_barrier fences keep that order):
+    // issued back to back they measured 2 % slower.
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_barrier(0);
       fa[1][j] = *(const bf16x8 *)(a_rd[1] + BUF * BM * kBK + j * 16 * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_16x16x32_tied(acc[0][j], fb[0][j], fa[0][0]);
+      __builtin_amdgcn_sched_barrier(0);
       fb[1][j] = *(const bf16x8 *)(b_rd[1] + BUF * BN * kBK + j * 16 * kBK);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
+      for (int i = 1; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
     }
     __builtin_amdgcn_sched_barrier(0);
     // this wave's reads of buffer BUF are done and its loads of stage kt+1
@@ -670,12 +675,21 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_barrier(0);
       fa[0][j] = *(const bf16x8 *)(a_rd[0] + (BUF ^ 1) * BM * kBK + j * 16 * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_16x16x32_tied(acc[0][j], fb[1][j], fa[1][0]);
+      __builtin_amdgcn_sched_barrier(0);
       fb[0][j] = *(const bf16x8 *)(b_rd[0] + (BUF ^ 1) * BN * kBK + j * 16 * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_16x16x32_tied(acc[1][j], fb[1][j], fa[1][1]);
+      __builtin_amdgcn_sched_barrier(0);
       load(fast, kt + 2, BUF, 2 * j);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_16x16x32_tied(acc[2][j], fb[1][j], fa[1][2]);
+      __builtin_amdgcn_sched_barrier(0);
       load(fast, kt + 2, BUF, 2 * j + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
+      for (int i = 3; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
