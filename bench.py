@@ -62,7 +62,7 @@ def _args():
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,"
-                   "bwd,f64,copy); copy is run only when named")
+                   "bwd,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
 
@@ -353,6 +353,25 @@ def bench_copy(steps, warmup):
             "read_bytes": n * 4, "write_bytes": n * 4}
 
 
+def bench_vendor(steps, warmup):
+    """torch.matmul (hipBLASLt) on the C2 inputs and on the bf16 shapes of C4
+    and C5: the vendor library's time for the same products, for comparison
+    only (run when named)."""
+    import torch
+    out = []
+    for (M, N, K, name) in ((4096, 4096, 4096, "c2"), (2048, 4096, 4096, "c4_shape_bf16"),
+                            (512, 22016, 4096, "c5_gateup_shape_bf16"),
+                            (512, 4096, 11008, "c5_down_shape_bf16")):
+        A = _rand_bf16((M, K), 1)
+        Bt = _rand_bf16((N, K), 2).t()
+        C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        ms = _time_launches(lambda i: torch.matmul(A, Bt, out=C), steps, warmup)
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out.append({"name": f"vendor_hipblaslt_{name}", "metric": f"torch.matmul bf16 {M}x{N}x{K}",
+                    "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms})
+    return out
+
+
 def cpu_baseline_c2(rows: int = 256):
     """The oracle's strict-k fp32 dot on upcast bf16 inputs (momijo's CPU
     engine applied to bf16 data, single thread) over `rows` rows of C2
@@ -396,8 +415,8 @@ def main():
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
                     ("c5", bench_c5), ("c1", bench_c1), ("bwd", bench_backward),
-                    ("f64", bench_f64), ("copy", bench_copy)):
-        if want(key) and (key != "copy" or "copy" in only):
+                    ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
+        if want(key) and (key not in ("copy", "vendor") or key in only):
             rs = fn(a.steps, a.warmup)
             for r in rs if isinstance(rs, list) else [rs]:
                 secondary.append(r)
