@@ -561,6 +561,13 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
   }
 }
 
+// s_waitcnt lgkmcnt(0) as the builtin (vmcnt and expcnt left open): unlike the
+// same text in inline asm, the compiler's wait-count pass sees it, so it does
+// not add a wait of its own for fragments this one already covered (such a
+// wait, placed after the next step's first read, stalled every stage for a
+// full LDS round trip).
+constexpr int kLgkm0 = 0xC07F;
+
 __device__ __forceinline__ void mfma_16x16x32_tied(f32x4 &acc, const bf16x8 &a, const bf16x8 &b) {
   asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
@@ -643,6 +650,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
 #pragma unroll
   for (int j = 0; j < TN; ++j) fb[0][j] = *(const bf16x8 *)(b_rd[0] + j * 16 * kBK);
+  // both ways into the K loop then arrive with no LDS read outstanding
+  __builtin_amdgcn_s_waitcnt(kLgkm0);
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
 
   // stage kt, held in buffer BUF (static: the loop is unrolled by two)
@@ -666,7 +675,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     __builtin_amdgcn_sched_barrier(0);
     // this wave's reads of buffer BUF are done and its loads of stage kt+1
     // have landed; after the barrier that holds for every wave
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     asm volatile("s_barrier" ::: "memory");
     // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the other buffer;
@@ -692,7 +701,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
       for (int i = 3; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
