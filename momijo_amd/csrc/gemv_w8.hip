@@ -50,7 +50,18 @@ __global__ __launch_bounds__(256) void gemv_w8a16_kernel(const uint16_t *__restr
     for (int i = wave; i < blocks; i += 4)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (gemv_lds_void *)(xs + i * 512), 16,
                                                (uint32_t)(i * 1024 + lane * 16), 0, 0, 0);
+    // the wait below counts on the x loads being issued before the weight
+    // loads: keep the scheduler from moving anything across this point
+    __builtin_amdgcn_sched_barrier(0);
   }
+
+  // the output lane of (row r, x row m) is r * MB + m: it fetches that row's
+  // scale and bias now, so no dependent load sits on the wave's tail (these
+  // loads precede the weight loads, which keeps the x-landed wait below exact)
+  const int my_r = lane / MB < RPW ? lane / MB : 0;
+  const int my_n = row0 + my_r < N ? row0 + my_r : N - 1;
+  const float my_s = scales[my_n];
+  const float my_b = bias ? bias[my_n] : 0.0f;
 
   float acc[RPW][MB];
 #pragma unroll
@@ -132,8 +143,8 @@ __global__ __launch_bounds__(256) void gemv_w8a16_kernel(const uint16_t *__restr
         float v;
         {
 #pragma clang fp contract(off)
-          v = s * scales[n];
-          if (bias) v = v + bias[n];
+          v = s * my_s;
+          if (bias) v = v + my_b;
         }
         v = apply_epi(epi, v);
         y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
