@@ -503,14 +503,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
 //    (the zero fill before the K loop and the epilogue's reads after it) are
 //    separated from the MFMAs by explicit s_nop cover; inside the loop each
 //    block is reused only every 64 MFMAs;
-//  * K advances 64 per stage through 2 LDS buffers of 128-byte rows (the
-//    XOR swizzle of swz()); every direct load fetches 128-byte row segments,
-//    half as many L2 requests as 32-deep stages would need;
+//  * K advances 64 per stage through 128-byte LDS rows (the XOR swizzle of
+//    swz()): 2 buffers for A and 3 for B, all 160 KB of LDS; every direct
+//    load fetches 128-byte row segments, half as many L2 requests as 32-deep
+//    stages would need;
 //  * each stage is two 32-deep MFMA steps, each step 8 groups of (2 fragment
-//    reads for the next step, 8 MFMAs).  The stage's one barrier sits between
-//    its two steps: there every wave holds the stage's fragments, so the
-//    stage's buffer is free, and the direct loads of stage kt+2 go into it
-//    during the second step (2 per group); they land two steps later;
+//    reads for the next step, 1 direct load, 8 MFMAs).  The stage's one
+//    barrier sits between its two steps: there every wave holds the stage's
+//    fragments, so the stage's A buffer is free and the A loads of stage kt+2
+//    go into it during the second step; the third B buffer (stage kt-1's,
+//    free since the previous barrier) takes the B loads of stage kt+2 during
+//    the first step.  8 loads per step instead of 16 in one step: with 16 the
+//    address unit could not keep up and stalled the wave's MFMA issue;
 //  * the K advance of a load is its scalar offset (no per-load VALU); the
 //    last stages, whose loads reach past K, take a per-load zero-fill select.
 //    The scalar offset stays below 2^31 and an out-of-range row offset plus it
@@ -577,8 +581,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   constexpr int WM = 128, WN = 128, TM = 8, TN = 8;
   constexpr int DPO = 8;  // 1-KB direct loads per wave per operand per stage
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t *As = lds;                    // [2][BM][64]
-  uint16_t *Bs = lds + 2 * BM * kBK;     // [2][BN][64]
+  uint16_t *As = lds;                    // [2][BM][64]: stage kt in buffer kt % 2
+  uint16_t *Bs = lds + 2 * BM * kBK;     // [3][BN][64]: stage kt in buffer kt % 3
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -606,8 +610,9 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     a_off[i] = m0 + r < M ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
     b_off[i] = n0 + r < N ? (uint32_t)((r * p.ldb + c * 8) * 2) : kOobOffset;
   }
-  // direct load d of stage kt into buffer buf: d < 8 is A block d, else B
-  // block d - 8.  FAST: the stage lies inside K.
+  // direct load d of stage kt into buffer buf (of A for d < 8, of B
+  // otherwise): d < 8 is A block d, else B block d - 8.  FAST: the stage lies
+  // inside K.
   auto load = [&](auto fast, int kt, int buf, int d) {
     const int k0 = kt * kBK;
     const int i = d & 7;
@@ -654,67 +659,84 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   __builtin_amdgcn_s_waitcnt(kLgkm0);
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
 
-  // stage kt, held in buffer BUF (static: the loop is unrolled by two)
-  auto stage = [&](auto buf_c, auto fast, int kt) {
-    constexpr int BUF = decltype(buf_c)::value;
-    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1].  Each
-    // read sits between two MFMAs (sched_barrier fences keep that order):
-    // issued back to back they measured 2 % slower.
+  // stage kt, held in A buffer AB = kt % 2 and B buffer BB = kt % 3 (static:
+  // the loop is unrolled by six)
+  auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
+    constexpr int AB = decltype(ab_c)::value;
+    constexpr int BB = decltype(bb_c)::value;
+    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1]; load B of
+    // stage kt+2 into B buffer (BB + 2) % 3, whose stage (kt-1) every wave
+    // finished reading before the previous stage's barrier.  Each read and
+    // load sits between two MFMAs (sched_barrier fences keep that order).
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_barrier(0);
-      fa[1][j] = *(const bf16x8 *)(a_rd[1] + BUF * BM * kBK + j * 16 * kBK);
+      fa[1][j] = *(const bf16x8 *)(a_rd[1] + AB * BM * kBK + j * 16 * kBK);
       __builtin_amdgcn_sched_barrier(0);
       mfma_16x16x32_tied(acc[0][j], fb[0][j], fa[0][0]);
       __builtin_amdgcn_sched_barrier(0);
-      fb[1][j] = *(const bf16x8 *)(b_rd[1] + BUF * BN * kBK + j * 16 * kBK);
+      fb[1][j] = *(const bf16x8 *)(b_rd[1] + BB * BN * kBK + j * 16 * kBK);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_16x16x32_tied(acc[1][j], fb[0][j], fa[0][1]);
+      __builtin_amdgcn_sched_barrier(0);
+      load(fast, kt + 2, (BB + 2) % 3, 8 + j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 1; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
+      for (int i = 2; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // this wave's reads of buffer BUF are done and its loads of stage kt+1
-    // have landed; after the barrier that holds for every wave
+    // this wave's reads of stage kt's buffers are done and its loads of
+    // stage kt+1 have landed (only the 8 B loads just issued may still be in
+    // flight: loads retire in order); after the barrier that holds for every
+    // wave
     __builtin_amdgcn_s_waitcnt(kLgkm0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | 8);  // vmcnt(8)
     asm volatile("s_barrier" ::: "memory");
-    // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the other buffer;
-    // load stage kt+2 into this one
+    // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the next buffers;
+    // load A of stage kt+2 into A buffer AB
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       __builtin_amdgcn_sched_barrier(0);
-      fa[0][j] = *(const bf16x8 *)(a_rd[0] + (BUF ^ 1) * BM * kBK + j * 16 * kBK);
+      fa[0][j] = *(const bf16x8 *)(a_rd[0] + (AB ^ 1) * BM * kBK + j * 16 * kBK);
       __builtin_amdgcn_sched_barrier(0);
       mfma_16x16x32_tied(acc[0][j], fb[1][j], fa[1][0]);
       __builtin_amdgcn_sched_barrier(0);
-      fb[0][j] = *(const bf16x8 *)(b_rd[0] + (BUF ^ 1) * BN * kBK + j * 16 * kBK);
+      fb[0][j] = *(const bf16x8 *)(b_rd[0] + ((BB + 1) % 3) * BN * kBK + j * 16 * kBK);
       __builtin_amdgcn_sched_barrier(0);
       mfma_16x16x32_tied(acc[1][j], fb[1][j], fa[1][1]);
       __builtin_amdgcn_sched_barrier(0);
-      load(fast, kt + 2, BUF, 2 * j);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_16x16x32_tied(acc[2][j], fb[1][j], fa[1][2]);
-      __builtin_amdgcn_sched_barrier(0);
-      load(fast, kt + 2, BUF, 2 * j + 1);
+      load(fast, kt + 2, AB, j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 3; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
+      for (int i = 2; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
     }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
   };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-  // stages kt and kt+1 load stages kt+2 and kt+3, inside K while kt+4 <= K/64
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using F = std::true_type;
+  using S = std::false_type;
+  // stages kt .. kt+5 load stages kt+2 .. kt+7, inside K while kt+8 <= K/64
   const int nk_full = K / kBK;
   int kt = 0;
-  for (; kt + 4 <= nk_full; kt += 2) {
-    stage(B0(), std::true_type(), kt);
-    stage(B1(), std::true_type(), kt + 1);
+  for (; kt + 8 <= nk_full; kt += 6) {
+    stage(I0(), I0(), F(), kt);
+    stage(I1(), I1(), F(), kt + 1);
+    stage(I0(), I2(), F(), kt + 2);
+    stage(I1(), I0(), F(), kt + 3);
+    stage(I0(), I1(), F(), kt + 4);
+    stage(I1(), I2(), F(), kt + 5);
   }
-  for (; kt < nk; kt += 2) {
-    stage(B0(), std::false_type(), kt);
-    if (kt + 1 < nk) stage(B1(), std::false_type(), kt + 1);
+  // the last stages (kt is a multiple of 6 here) take the zero-fill loads
+  for (; kt < nk; kt += 6) {
+    stage(I0(), I0(), S(), kt);
+    if (kt + 1 < nk) stage(I1(), I1(), S(), kt + 1);
+    if (kt + 2 < nk) stage(I0(), I2(), S(), kt + 2);
+    if (kt + 3 < nk) stage(I1(), I0(), S(), kt + 3);
+    if (kt + 4 < nk) stage(I0(), I1(), S(), kt + 4);
+    if (kt + 5 < nk) stage(I1(), I2(), S(), kt + 5);
   }
   // last MFMAs -> the epilogue's accumulator reads; the zero-filled loads of
   // the two stages past the end target LDS that the epilogue reuses
@@ -830,7 +852,7 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
 }
 
 static hipError_t launch_w4(const GemmNT &p, hipStream_t stream) {
-  constexpr size_t lds_loop = size_t(2) * (256 + 256) * kBK * sizeof(uint16_t);
+  constexpr size_t lds_loop = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
   constexpr size_t lds_out = size_t(256) * stage_ld<256>() * sizeof(uint16_t);
   constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   static_assert(lds <= 160 * 1024, "LDS budget");
