@@ -507,8 +507,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
 //    swz()): 2 buffers for A and 3 for B, all 160 KB of LDS; every direct
 //    load fetches 128-byte row segments, half as many L2 requests as 32-deep
 //    stages would need;
-//  * each stage is two 32-deep MFMA steps, each step 8 groups of (2 fragment
-//    reads for the next step, 1 direct load, 8 MFMAs).  The stage's one
+//  * each stage is two 32-deep MFMA steps, each step 8 groups of 8 MFMAs with
+//    the step's 16 fragment reads for the next step spread 3,3,3,3,2,2 over
+//    the first six groups (the last lands 16 MFMAs before the wait that needs
+//    it) and one direct load per group.  The stage's one
 //    barrier sits between its two steps: there every wave holds the stage's
 //    fragments, so the stage's A buffer is free and the A loads of stage kt+2
 //    go into it during the second step; the third B buffer (stage kt-1's,
@@ -664,26 +666,34 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
     constexpr int AB = decltype(ab_c)::value;
     constexpr int BB = decltype(bb_c)::value;
+    // the 16 fragment reads of a step go 3, 3, 3, 3, 2, 2 into groups 0-5
+    // (read t < 8: A block t, else B block t - 8), so the last lands 16 MFMAs
+    // before the wait that needs it
+    auto read_frag = [&](int t, int dst, int abuf, int bbuf) {
+      if (t < 8) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
+      else fb[dst][t - 8] = *(const bf16x8 *)(b_rd[dst] + bbuf * BN * kBK + (t - 8) * 16 * kBK);
+    };
+    auto group = [&](int j, int src, int dst, int abuf, int bbuf, int load_d, int load_buf) {
+      const int t0 = j < 4 ? 3 * j : 12 + 2 * (j - 4);
+      const int nt = j < 4 ? 3 : (j < 6 ? 2 : 0);
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (u < nt) read_frag(t0 + u, dst, abuf, bbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_16x16x32_tied(acc[u][j], fb[src][j], fa[src][u]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load(fast, kt + 2, load_buf, load_d);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 3; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[src][j], fa[src][i]);
+    };
     // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1]; load B of
     // stage kt+2 into B buffer (BB + 2) % 3, whose stage (kt-1) every wave
-    // finished reading before the previous stage's barrier.  Each read and
-    // load sits between two MFMAs (sched_barrier fences keep that order).
+    // finished reading before the previous stage's barrier
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      fa[1][j] = *(const bf16x8 *)(a_rd[1] + AB * BM * kBK + j * 16 * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_16x16x32_tied(acc[0][j], fb[0][j], fa[0][0]);
-      __builtin_amdgcn_sched_barrier(0);
-      fb[1][j] = *(const bf16x8 *)(b_rd[1] + BB * BN * kBK + j * 16 * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_16x16x32_tied(acc[1][j], fb[0][j], fa[0][1]);
-      __builtin_amdgcn_sched_barrier(0);
-      load(fast, kt + 2, (BB + 2) % 3, 8 + j);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 2; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[0][j], fa[0][i]);
-    }
+    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, 8 + j, (BB + 2) % 3);
     __builtin_amdgcn_sched_barrier(0);
     // this wave's reads of stage kt's buffers are done and its loads of
     // stage kt+1 have landed (only the 8 B loads just issued may still be in
@@ -695,21 +705,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the next buffers;
     // load A of stage kt+2 into A buffer AB
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      fa[0][j] = *(const bf16x8 *)(a_rd[0] + (AB ^ 1) * BM * kBK + j * 16 * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_16x16x32_tied(acc[0][j], fb[1][j], fa[1][0]);
-      __builtin_amdgcn_sched_barrier(0);
-      fb[0][j] = *(const bf16x8 *)(b_rd[0] + ((BB + 1) % 3) * BN * kBK + j * 16 * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_16x16x32_tied(acc[1][j], fb[1][j], fa[1][1]);
-      __builtin_amdgcn_sched_barrier(0);
-      load(fast, kt + 2, AB, j);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 2; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[1][j], fa[1][i]);
-    }
+    for (int j = 0; j < TN; ++j) group(j, 1, 0, AB ^ 1, (BB + 1) % 3, j, AB);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
   };
