@@ -567,6 +567,51 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
   }
 }
 
+// Gate/up epilogue of a full, aligned tile straight from the accumulators:
+// h = silu32(g*sg) * (u*su) for blocks j < TN/2 (gate) and j + TN/2 (up),
+// then the same permlane pairing as store_tile_direct over the TN/2 output
+// blocks.
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4 (&acc)[TM][TN],
+                                                    int m0, int n0, int wm, int wn, int lane) {
+  constexpr int TO = TN / 2;
+  static_assert(TO % 2 == 0, "output blocks are stored in pairs");
+  const int fr = lane & 15, fh = lane >> 4;
+  float sg[TO][4], su[TO][4];
+#pragma unroll
+  for (int j = 0; j < TO; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wn * (WN / 2) + j * 16 + 4 * fh + q;
+      sg[j][q] = p.scales[n];
+      su[j][q] = p.scales2[n];
+    }
+#pragma unroll
+  for (int j = 0; j < TO; j += 2) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float x[4], y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+        const float g0 = epi_scale_bias(acc[i][j][q], sg[j][q], 0.0f, true, false);
+        const float u0 = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
+        const float g1 = epi_scale_bias(acc[i][j + 1][q], sg[j + 1][q], 0.0f, true, false);
+        const float u1 = epi_scale_bias(acc[i][j + 1 + TO][q], su[j + 1][q], 0.0f, true, false);
+        x[q] = silu32(g0) * u0;
+        y[q] = silu32(g1) * u1;
+      }
+      const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
+                                                       pack_bf16x2(y[0], y[1]), false, false);
+      const auto w1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[2], x[3]),
+                                                       pack_bf16x2(y[2], y[3]), false, false);
+      const int m = m0 + wm * WM + i * 16 + fr;
+      const int n = n0 + wn * (WN / 2) + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
+      *(uint4 *)(p.C + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
+    }
+  }
+}
+
 // s_waitcnt lgkmcnt(0) as the builtin (vmcnt and expcnt left open): unlike the
 // same text in inline asm, the compiler's wait-count pass sees it, so it does
 // not add a wait of its own for fragments this one already covered (such a
@@ -775,6 +820,336 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   flush_tile<BM, BN, NT>(p, ct, m0, n0);
 }
 
+// ---------------------------------------------------------------------------
+// W8A16 tiles with one wave per SIMD: A bf16, B int8 per-channel weights.
+// The same pipeline as gemm_nt_w4_kernel (2 A buffers of 128-byte rows, 3 B
+// buffers, one barrier between the two 32-deep steps of a 64-deep stage, the
+// stage's direct loads spread one per MFMA group), with the weights kept int8
+// all the way into registers:
+//  * B rows are 64 bytes per stage in LDS, filled by direct loads (16 rows per
+//    1-KB load); the 16-byte chunk c of row r is stored at c ^ ((r >> 2) & 3);
+//  * a lane's B fragment of a 32-deep step is 8 int8 (one ds_read_b64 at
+//    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 (SDWA
+//    convert to fp32, v_cvt_pk_bf16_f32; |q| <= 127 is exact in bf16) one MFMA
+//    group before its MFMAs use it;
+//  * BN = 256 (waves 128 x 128) or 128 (waves 128 x 64); GATEUP pairs each
+//    wave's WN/2 gate rows with the WN/2 up rows of the same output columns
+//    (blocks j and j + TN/2), as gemm_nt_kernel does;
+//  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
+//    compiler put a full vmcnt(0) before each of them, which took away the
+//    load pipelining and doubled the kernel's time;
+//  * split-K: workgroup (split, tile) runs its K slice into fp32 partials,
+//    reduced by splitk_reduce_kernel.
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+
+// LDS read of 8 bytes as inline asm.  The compiler's wait-count pass cannot
+// tell such a read from the direct loads still in flight into other LDS
+// buffers and, for a C++ read, waits for all of them (vmcnt(0)) before it;
+// the kernel's own waits (the per-stage vmcnt and barrier) already order every
+// read after the loads it needs.  The result is not tracked by the compiler,
+// which treats the register as written at once: the caller waits (lgkmcnt)
+// and then marks the register landed().
+__device__ __forceinline__ uint2 ds_read8_asm(uint32_t addr) {
+  uint2 r;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// Placed after the wait for an asm read: an empty asm that takes the register
+// as read-written, so no use of the value (and no reuse of the register) can
+// be moved ahead of the wait, not even by IR passes, which see the wait as an
+// unrelated call.
+__device__ __forceinline__ void landed(uint2 &r) { asm volatile("" : "+v"(r)); }
+
+__device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 q) {
+  const uint32_t w[2] = {q.x, q.y};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int32_t v = (int32_t)w[i];
+    o[2 * i] = pack_bf16x2((float)((v << 24) >> 24), (float)((v << 16) >> 24));
+    o[2 * i + 1] = pack_bf16x2((float)((v << 8) >> 24), (float)(v >> 24));
+  }
+  return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+template <int BN, bool GATEUP>
+__global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
+  constexpr int BM = 256, NT = 256;
+  constexpr int WM = 128, WN = BN / 2, TM = 8, TN = WN / 16;
+  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
+  constexpr int A_DPW = 8;                   // 1-KB A loads per wave per stage
+  constexpr int B_DPW = BN / 64;             // 1-KB B loads per wave per stage (16 rows each)
+  constexpr int BROW = 64;                   // int8 B row bytes per stage
+  static_assert(!GATEUP || TN % 2 == 0, "gate/up pairs blocks j and j + TN/2");
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  uint16_t *As = lds;                                        // [2][BM][64] bf16
+  int8_t *Bs = (int8_t *)(lds + 2 * BM * kBK);               // [3][BN][64] int8
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN_OUT - 1) / BN_OUT;
+  const int tiles = tiles_m * tiles_n;
+  const int split = blockIdx.x / tiles;
+  int tm, tn;
+  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, 4, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN_OUT;
+  const int nk_all = (K + kBK - 1) / kBK;
+  const int per = (nk_all + p.splits - 1) / p.splits;
+  const int kt0 = split * per;
+  const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
+  const int Kend = kt1 * kBK < K ? kt1 * kBK : K;  // loads stop here (zero fill beyond)
+
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(p.A + (size_t)m0 * p.lda,
+                                              ((int64_t)(M - m0) * p.lda) * 2);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(p.B, (int64_t)N * p.ldb);
+  const __amdgpu_buffer_rsrc_t rB2 = make_rsrc(GATEUP ? p.B2 : p.B, (int64_t)N * p.ldb);
+  uint32_t a_off[A_DPW];
+  int a_kc[A_DPW];
+#pragma unroll
+  for (int i = 0; i < A_DPW; ++i) {
+    const int r = (i * 4 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_kc[i] = c;
+    a_off[i] = m0 + r < M ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
+  }
+  // B block b = i*4 + wave covers LDS rows [16b, 16b+16): row 16b + lane/4,
+  // stored chunk lane%4 holds logical chunk c of the weight row
+  uint32_t b_off[B_DPW];
+  int b_kc[B_DPW];
+  bool b_up[B_DPW];
+#pragma unroll
+  for (int i = 0; i < B_DPW; ++i) {
+    const int r = (i * 4 + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    int n = n0 + r;
+    b_up[i] = false;
+    if (GATEUP) {
+      const int w = r / WN, rr = r % WN;
+      b_up[i] = rr >= WN / 2;
+      n = n0 + w * (WN / 2) + rr % (WN / 2);
+    }
+    b_kc[i] = c;
+    b_off[i] = n < N ? (uint32_t)((size_t)n * p.ldb + c * 16) : kOobOffset;
+  }
+  // direct load d of stage kt: d < 8 is A block d into A buffer abuf, else B
+  // block d - 8 into B buffer bbuf.  FAST: the stage lies inside the K slice.
+  auto load = [&](auto fast, int kt, int buf, int d) {
+    const int k0 = kt * kBK;
+    if (d < A_DPW) {
+      uint16_t *dst = As + buf * BM * kBK + (d * 4 + wave) * 8 * kBK;
+      if constexpr (decltype(fast)::value) {
+        dma16s(rA, dst, a_off[d], (uint32_t)(k0 * 2));
+      } else {
+        const bool ok = k0 + a_kc[d] * 8 < Kend;
+        dma16s(rA, dst, ok ? a_off[d] + k0 * 2 : kOobOffset, 0u);
+      }
+    } else {
+      const int i = d - A_DPW;
+      uint16_t *dst = (uint16_t *)(Bs + buf * BN * BROW + (i * 4 + wave) * 16 * BROW);
+      const __amdgpu_buffer_rsrc_t r = (GATEUP && b_up[i]) ? rB2 : rB;
+      if constexpr (decltype(fast)::value) {
+        dma16s(r, dst, b_off[i], (uint32_t)k0);
+      } else {
+        const bool ok = k0 + b_kc[i] * 16 < Kend;
+        dma16s(r, dst, ok ? b_off[i] + k0 : kOobOffset, 0u);
+      }
+    }
+  };
+
+  const int fr = lane & 15, fh = lane >> 4;
+  const int sw = (fr >> 1) & 7;
+  const uint16_t *a_rd[2];
+  uint32_t b_rd[2];  // LDS byte addresses
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    a_rd[ks] = As + (wm * WM + fr) * kBK + ((ks * 4 + fh) ^ sw) * 8;
+    // rows of a wave's B blocks start at multiples of 16, so (r >> 2) & 3 is
+    // (fr >> 2) & 3
+    b_rd[ks] = (uint32_t)(uintptr_t)(lds_u8 *)(Bs + (wn * WN + fr) * BROW +
+                                               (((ks * 4 + fh) ^ (2 * ((fr >> 2) & 3)))) * 8);
+  }
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8 fa[2][TM];
+  uint2 fbr[2][TN];  // raw int8 B fragments
+  bf16x8 fbc[2];     // widened B fragment of the current and the next group
+
+  constexpr int NDMA = A_DPW + B_DPW;
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int d = 0; d < NDMA; ++d) load(std::false_type(), kt0 + s2, s2, d);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));  // stage kt0
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fbr[0][j] = ds_read8_asm(b_rd[0] + j * 16 * BROW);
+  __builtin_amdgcn_s_waitcnt(kLgkm0);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) landed(fbr[0][j]);
+  fbc[0] = i8x8_to_bf16x8(fbr[0][0]);
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
+
+  // one 32-deep step: MFMAs on fa[src] and the widened fbr[src]; the step's
+  // TM + TN fragment reads for the next step (into fa/fbr[dst], from A buffer
+  // abuf and B buffer bbuf) are spread over its groups, and its nload direct
+  // loads (load_d, load_d + 1, ...) into buffer load_buf over its first groups
+  // (every index argument is a compile-time constant, so the fragment arrays
+  // stay in registers and the LDS pointers keep their address space)
+  auto step = [&](auto src_c, auto dst_c, auto abuf_c, auto bbuf_c, auto fast, int kt,
+                  auto load_d_c, auto nload_c, auto load_buf_c) {
+    constexpr int src = decltype(src_c)::value, dst = decltype(dst_c)::value;
+    constexpr int abuf = decltype(abuf_c)::value, bbuf = decltype(bbuf_c)::value;
+    constexpr int load_d = decltype(load_d_c)::value, nload = decltype(nload_c)::value;
+    constexpr int load_buf = decltype(load_buf_c)::value;
+    constexpr int NR = TM + TN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int t0 = (j * NR + TN - 1) / TN;
+      const int t1 = ((j + 1) * NR + TN - 1) / TN;
+#pragma unroll
+      for (int u = 0; u < TM; ++u) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int t = t0 + u;
+        if (t < t1) {
+          if (t < TM) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
+          else fbr[dst][t - TM] = ds_read8_asm(b_rd[dst] + bbuf * BN * BROW + (t - TM) * 16 * BROW);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_16x16x32_tied(acc[u][j], fbc[j & 1], fa[src][u]);
+        if (u == 1 || u == 2) {
+          // loads per group: ceil(nload / TN), the first at u = 1
+          const int lpg = (nload + TN - 1) / TN;
+          const int l = j * lpg + (u - 1);
+          __builtin_amdgcn_sched_barrier(0);
+          if (u - 1 < lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (u == 3) {
+          // widen the next group's B fragment; the last group widens the
+          // next step's first (read in this step).  Either way four MFMAs
+          // separate the VALU writes from the first MFMA that reads them: the
+          // asm MFMAs are invisible to the compiler's hazard recognizer, so
+          // that distance is what covers the VALU -> MFMA operand hazard
+          __builtin_amdgcn_sched_barrier(0);
+          if (j + 1 < TN) {
+            fbc[(j + 1) & 1] = i8x8_to_bf16x8(fbr[src][j + 1]);
+          } else {
+            // fbr[dst][0] is this step's read t = TM; the TN - 1 reads after
+            // it may still be in flight
+            __builtin_amdgcn_s_waitcnt(kLgkm0 | ((TN - 1) << 8));
+            landed(fbr[dst][0]);
+            fbc[0] = i8x8_to_bf16x8(fbr[dst][0]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+  // stage kt in A buffer AB = (kt - kt0) % 2 and B buffer BB = (kt - kt0) % 3
+  auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
+    constexpr int AB = decltype(ab_c)::value;
+    constexpr int BB = decltype(bb_c)::value;
+    // step 0; loads of B for stage kt+2 go into B buffer (BB + 2) % 3
+    step(IC<0>(), IC<1>(), IC<AB>(), IC<BB>(), fast, kt, IC<A_DPW>(), IC<B_DPW>(),
+         IC<(BB + 2) % 3>());
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+#pragma unroll
+    for (int j = 1; j < TN; ++j) landed(fbr[1][j]);
+    // only this stage's B loads may be in flight (loads retire in order)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | B_DPW);
+    asm volatile("s_barrier" ::: "memory");
+    // step 1; loads of A for stage kt+2 go into A buffer AB
+    step(IC<1>(), IC<0>(), IC<AB ^ 1>(), IC<(BB + 1) % 3>(), fast, kt, IC<0>(), IC<A_DPW>(),
+         IC<AB>());
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+#pragma unroll
+    for (int j = 1; j < TN; ++j) landed(fbr[0][j]);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using F = std::true_type;
+  using S = std::false_type;
+  // stages kt .. kt+5 load stages kt+2 .. kt+7: fast while those lie inside K
+  const int full_end = kt0 + (Kend - kt0 * kBK) / kBK;  // stages wholly inside the slice
+  int kt = kt0;
+  for (; kt + 8 <= full_end; kt += 6) {
+    stage(I0(), I0(), F(), kt);
+    stage(I1(), I1(), F(), kt + 1);
+    stage(I0(), I2(), F(), kt + 2);
+    stage(I1(), I0(), F(), kt + 3);
+    stage(I0(), I1(), F(), kt + 4);
+    stage(I1(), I2(), F(), kt + 5);
+  }
+  for (; kt < kt1; kt += 6) {
+    stage(I0(), I0(), S(), kt);
+    if (kt + 1 < kt1) stage(I1(), I1(), S(), kt + 1);
+    if (kt + 2 < kt1) stage(I0(), I2(), S(), kt + 2);
+    if (kt + 3 < kt1) stage(I1(), I0(), S(), kt + 3);
+    if (kt + 4 < kt1) stage(I0(), I1(), S(), kt + 4);
+    if (kt + 5 < kt1) stage(I1(), I2(), S(), kt + 5);
+  }
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+
+  if (p.part != nullptr) {
+    if constexpr (!GATEUP) store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, split);
+    return;
+  }
+  const bool full = m0 + BM <= M && n0 + BN_OUT <= N && (p.ldc & 7) == 0 &&
+                    ((uintptr_t)p.C & 15) == 0;
+  if constexpr (GATEUP) {
+    if (full) {
+      store_gateup_direct<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane);
+      return;
+    }
+    stage_gateup<TM, TN, WM, WN, BN_OUT>(p, acc, lds, n0, wm, wn, lane);
+  } else {
+    if (full) {
+      switch (p.epi) {
+#define MJ_DIRECT(E) store_tile_direct<E, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
+        case EPI_RELU: MJ_DIRECT(EPI_RELU)
+        case EPI_GELU_TANH: MJ_DIRECT(EPI_GELU_TANH)
+        case EPI_SILU: MJ_DIRECT(EPI_SILU)
+        case EPI_GELU_TANH_APPROX: MJ_DIRECT(EPI_GELU_TANH_APPROX)
+        case EPI_SILU_APPROX: MJ_DIRECT(EPI_SILU_APPROX)
+        case EPI_RELU_UNARY: MJ_DIRECT(EPI_RELU_UNARY)
+        default: MJ_DIRECT(EPI_NONE)
+#undef MJ_DIRECT
+      }
+      return;
+    }
+    switch (p.epi) {
+#define MJ_STAGE(E) stage_tile<E, TM, TN, WM, WN, BN_OUT>(p, acc, lds, n0, wm, wn, lane); break;
+      case EPI_RELU: MJ_STAGE(EPI_RELU)
+      case EPI_GELU_TANH: MJ_STAGE(EPI_GELU_TANH)
+      case EPI_SILU: MJ_STAGE(EPI_SILU)
+      case EPI_GELU_TANH_APPROX: MJ_STAGE(EPI_GELU_TANH_APPROX)
+      case EPI_SILU_APPROX: MJ_STAGE(EPI_SILU_APPROX)
+      case EPI_RELU_UNARY: MJ_STAGE(EPI_RELU_UNARY)
+      default: MJ_STAGE(EPI_NONE)
+#undef MJ_STAGE
+    }
+  }
+  __syncthreads();
+  flush_tile<BM, BN_OUT, NT>(p, lds, m0, n0);
+}
+
 // Sums the split-K partials in split order and applies scale, bias, the
 // activation and the bf16 rounding; 4 columns per thread.
 template <int E>
@@ -869,6 +1244,35 @@ static hipError_t launch_w4(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int BN, bool GATEUP>
+static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
+  constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
+  constexpr size_t lds_loop = size_t(2) * 256 * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
+  constexpr size_t lds_out = size_t(256) * stage_ld<BN_OUT>() * sizeof(uint16_t);
+  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  // buffer offsets: A rows of the tile and every weight row must stay within
+  // 31-bit offsets, K advances in the scalar offset
+  if (p.K >= ((int64_t)1 << 30) || p.bkind != B_INT8 || p.gate_up != GATEUP ||
+      p.N * p.ldb >= ((int64_t)1 << 31) || 256 * p.lda * 2 >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  auto kern = gemm_nt_w4i8_kernel<BN, GATEUP>;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  const int64_t grid = ((p.M + 255) / 256) * ((p.N + BN_OUT - 1) / BN_OUT) * p.splits;
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
 template <int BKIND, bool IGLP, bool PF2>
 static hipError_t launch_plain(int bm, int bn, const GemmNT &p, hipStream_t stream) {
   if (bm == 256 && bn == 256) return launch_tile<256, 256, BKIND, false, IGLP, PF2>(p, stream);
@@ -935,10 +1339,31 @@ static double plan_time_us(const GemmNT &p, int bm, int bn, int splits) {
 
 GemmPlan plan_gemm_nt(const GemmNT &p) {
   GemmPlan pl;
+  // the one-wave-per-SIMD int8 kernel needs 31-bit weight offsets and K < 2^30
+  const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
+                       p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
   if (p.gate_up) {
-    // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up
+    // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up.
+    // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
+    // and up: 20 us faster than the 8-wave kernel)
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
+    pl.wave4 = pl.bm == 256 && w4i8_ok;
+    return pl;
+  }
+  if (w4i8_ok && p.M >= 256) {
+    // the one-wave-per-SIMD int8 kernel on 256 x 128 tiles, K split until the
+    // grid covers the 256 CUs (>= 8 stages per split).  Measured on MI355X:
+    // 2048x4096x4096 71 us (8-wave 128 x 256: 83 us; 256 x 256 tiles, which
+    // leave half the CUs idle: 126 us, split in two: 102 us); the 512 x 4096 x
+    // 11008 down projection 4-way split beats 2- and 8-way
+    pl.bm = 256;
+    pl.bn = 128;
+    pl.wave4 = true;
+    const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
+    const int64_t nk = (p.K + kBK - 1) / kBK;
+    while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
+      pl.splits *= 2;
     return pl;
   }
   const int64_t nk = (p.K + kBK - 1) / kBK;
@@ -975,6 +1400,10 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.splits = 1;
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
+    if (pl.wave4) {
+      if (pl.bm != 256 || pl.bn != 256) return hipErrorInvalidValue;
+      return launch_w4i8<256, true>(p, stream);
+    }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
   }
@@ -998,6 +1427,9 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
       e = launch_tile<256, 128, B_BF16, false, true, true>(p, stream);
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
+  } else if (pl.wave4) {
+    if (pl.bm != 256 || (pl.bn != 128 && pl.bn != 256)) return hipErrorInvalidValue;
+    e = pl.bn == 128 ? launch_w4i8<128, false>(p, stream) : launch_w4i8<256, false>(p, stream);
   } else {
     if (pl.pf2) return hipErrorInvalidValue;
     e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)

@@ -36,7 +36,7 @@ struct GemmPlan {
   int bm = 256, bn = 256, splits = 1;
   bool iglp = false;  // K loop built with the compiler's MFMA interleave
   bool pf2 = false;   // distance-2 load pipeline (bf16 B)
-  bool wave4 = false; // bf16 256 x 256: one wave per SIMD, 128 x 128 per wave
+  bool wave4 = false; // one wave per SIMD: bf16 256 x 256, int8 256 x 128 / 256 x 256
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
   }
