@@ -863,6 +863,17 @@ __device__ __forceinline__ uint2 ds_read8_asm(uint32_t addr) {
 // unrelated call.
 __device__ __forceinline__ void landed(uint2 &r) { asm volatile("" : "+v"(r)); }
 
+// Quarter p of i8x8_to_bf16x8: int8 2p and 2p+1 of the 8 in q as bf16x2.
+// An integer of magnitude <= 128 has at most 8 significant bits, so its bf16
+// is exactly the upper half of its fp32: one byte permute packs two (an
+// integer op, cheaper beside the MFMAs than the float convert-and-pack).
+__device__ __forceinline__ uint32_t i8x8_quarter(uint2 q, int p) {
+  const int32_t v = (int32_t)(p < 2 ? q.x : q.y);
+  const float lo = (p & 1) ? (float)((v << 8) >> 24) : (float)((v << 24) >> 24);
+  const float hi = (p & 1) ? (float)(v >> 24) : (float)((v << 16) >> 24);
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
 __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 q) {
   const uint32_t w[2] = {q.x, q.y};
   uint32_t o[4];
@@ -981,8 +992,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   bf16x8 fa[2][TM];
-  uint2 fbr[2][TN];  // raw int8 B fragments
-  bf16x8 fbc[2];     // widened B fragment of the current and the next group
+  uint2 fbr[2][TN];      // raw int8 B fragments
+  uint32_t fbc[2][4];    // widened B fragment (bf16x2 words) of this and the next group
 
   constexpr int NDMA = A_DPW + B_DPW;
 #pragma unroll
@@ -992,21 +1003,29 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));  // stage kt0
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
-#pragma unroll
   for (int j = 0; j < TN; ++j) fbr[0][j] = ds_read8_asm(b_rd[0] + j * 16 * BROW);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
   __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
   for (int j = 0; j < TN; ++j) landed(fbr[0][j]);
-  fbc[0] = i8x8_to_bf16x8(fbr[0][0]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) fbc[0][q] = i8x8_quarter(fbr[0][0], q);
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
 
   // one 32-deep step: MFMAs on fa[src] and the widened fbr[src]; the step's
-  // TM + TN fragment reads for the next step (into fa/fbr[dst], from A buffer
-  // abuf and B buffer bbuf) are spread over its groups, and its nload direct
-  // loads (load_d, load_d + 1, ...) into buffer load_buf over its first groups
-  // (every index argument is a compile-time constant, so the fragment arrays
-  // stay in registers and the LDS pointers keep their address space)
+  // TN + TM fragment reads for the next step (B first, into fbr/fa[dst], from
+  // B buffer bbuf and A buffer abuf) are spread over its groups, and its nload
+  // direct loads (load_d, load_d + 1, ...) into buffer load_buf over its first
+  // groups.  Group j widens the B fragment of group j + 1 (the last group: the
+  // next step's first, read at the start of this step) in four quarters of
+  // three VALU ops after its first four MFMAs, so the conversion hides under
+  // the MFMAs instead of stalling their issue, and four MFMAs separate the
+  // last VALU write from the first MFMA that reads it (the asm MFMAs are
+  // invisible to the compiler's hazard recognizer; that distance covers the
+  // VALU -> MFMA operand hazard).  Every index argument is a compile-time
+  // constant, so the fragment arrays stay in registers and the LDS pointers
+  // keep their address space.
   auto step = [&](auto src_c, auto dst_c, auto abuf_c, auto bbuf_c, auto fast, int kt,
                   auto load_d_c, auto nload_c, auto load_buf_c) {
     constexpr int src = decltype(src_c)::value, dst = decltype(dst_c)::value;
@@ -1023,11 +1042,14 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
         __builtin_amdgcn_sched_barrier(0);
         const int t = t0 + u;
         if (t < t1) {
-          if (t < TM) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
-          else fbr[dst][t - TM] = ds_read8_asm(b_rd[dst] + bbuf * BN * BROW + (t - TM) * 16 * BROW);
+          if (t < TN) fbr[dst][t] = ds_read8_asm(b_rd[dst] + bbuf * BN * BROW + t * 16 * BROW);
+          else fa[dst][t - TN] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + (t - TN) * 16 * kBK);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfma_16x16x32_tied(acc[u][j], fbc[j & 1], fa[src][u]);
+        mfma_16x16x32_tied(acc[u][j],
+                           __builtin_bit_cast(bf16x8, make_uint4(fbc[j & 1][0], fbc[j & 1][1],
+                                                                 fbc[j & 1][2], fbc[j & 1][3])),
+                           fa[src][u]);
         if (u == 1 || u == 2) {
           // loads per group: ceil(nload / TN), the first at u = 1
           const int lpg = (nload + TN - 1) / TN;
@@ -1036,21 +1058,20 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
           if (u - 1 < lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (u == 3) {
-          // widen the next group's B fragment; the last group widens the
-          // next step's first (read in this step).  Either way four MFMAs
-          // separate the VALU writes from the first MFMA that reads them: the
-          // asm MFMAs are invisible to the compiler's hazard recognizer, so
-          // that distance is what covers the VALU -> MFMA operand hazard
+        if (u < 4) {
           __builtin_amdgcn_sched_barrier(0);
           if (j + 1 < TN) {
-            fbc[(j + 1) & 1] = i8x8_to_bf16x8(fbr[src][j + 1]);
+            fbc[(j + 1) & 1][u] = i8x8_quarter(fbr[src][j + 1], u);
           } else {
-            // fbr[dst][0] is this step's read t = TM; the TN - 1 reads after
-            // it may still be in flight
-            __builtin_amdgcn_s_waitcnt(kLgkm0 | ((TN - 1) << 8));
-            landed(fbr[dst][0]);
-            fbc[0] = i8x8_to_bf16x8(fbr[dst][0]);
+            if (u == 0) {
+              // fbr[dst][0] is this step's first read; the reads issued
+              // after it (t = 1 .. t0 of this group) may still be in flight
+              constexpr int kAfter = ((TN - 1) * NR + TN - 1) / TN;
+              static_assert(kAfter <= 15, "lgkmcnt field");
+              __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
+              landed(fbr[dst][0]);
+            }
+            fbc[0][u] = i8x8_quarter(fbr[dst][0], u);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
