@@ -1172,14 +1172,50 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
 }
 
 // Sums the split-K partials in split order and applies scale, bias, the
-// activation and the bf16 rounding; 4 columns per thread.
+// activation and the bf16 rounding.  Rows of a multiple of 8 columns with a
+// 16-byte aligned output take 8 columns per thread: all of the thread's
+// partial loads (two 16-byte nontemporal loads per split) are issued before
+// the sums, and the result is one 16-byte store; anything else takes 4
+// columns per thread.
 template <int E>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
   const int M = (int)p.M, N = (int)p.N;
-  const int n4 = (N + 3) / 4;
-  const int64_t total = (int64_t)M * n4;
   const size_t plane = (size_t)M * N;
   const bool has_s = p.scales != nullptr, has_b = p.bias != nullptr;
+  if ((N & 7) == 0 && (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0 && p.splits <= 8) {
+    const int n8 = N / 8;
+    const int64_t total8 = (int64_t)M * n8;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total8;
+         t += (int64_t)gridDim.x * blockDim.x) {
+      const int m = (int)(t / n8);
+      const int nb = (int)(t - (int64_t)m * n8) * 8;
+      const float *src = p.part + (size_t)m * N + nb;
+      f32x4 part[8][2];
+#pragma unroll
+      for (int sp = 0; sp < 8; ++sp) {
+        if (sp < p.splits) {
+          part[sp][0] = __builtin_nontemporal_load((const f32x4 *)(src + sp * plane));
+          part[sp][1] = __builtin_nontemporal_load((const f32x4 *)(src + sp * plane + 4));
+        }
+      }
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < 8; ++sp)
+          if (sp < p.splits) acc += part[sp][q >> 2][q & 3];
+        v[q] = apply_epi(E, epi_scale_bias(acc, has_s ? p.scales[nb + q] : 1.0f,
+                                           has_b ? p.bias[nb + q] : 0.0f, has_s, has_b));
+      }
+      *(uint4 *)(p.C + (size_t)m * p.ldc + nb) =
+          make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                     pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+    }
+    return;
+  }
+  const int n4 = (N + 3) / 4;
+  const int64_t total = (int64_t)M * n4;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int m = (int)(t / n4);
