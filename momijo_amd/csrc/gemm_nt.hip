@@ -570,12 +570,11 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
 // Gate/up epilogue of a full, aligned tile straight from the accumulators:
 // h = silu32(g*sg) * (u*su) for blocks j < TN/2 (gate) and j + TN/2 (up),
 // then the same permlane pairing as store_tile_direct over the TN/2 output
-// blocks.
+// blocks; an odd last block is stored 8 bytes (4 columns) per lane.
 template <int TM, int TN, int WM, int WN>
 __device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4 (&acc)[TM][TN],
                                                     int m0, int n0, int wm, int wn, int lane) {
   constexpr int TO = TN / 2;
-  static_assert(TO % 2 == 0, "output blocks are stored in pairs");
   const int fr = lane & 15, fh = lane >> 4;
   float sg[TO][4], su[TO][4];
 #pragma unroll
@@ -586,8 +585,26 @@ __device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4
       sg[j][q] = p.scales[n];
       su[j][q] = p.scales2[n];
     }
+  if constexpr (TO % 2 == 1) {
+    constexpr int j = TO - 1;
 #pragma unroll
-  for (int j = 0; j < TO; j += 2) {
+    for (int i = 0; i < TM; ++i) {
+      float h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+        const float g = epi_scale_bias(acc[i][j][q], sg[j][q], 0.0f, true, false);
+        const float u = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
+        h[q] = silu32(g) * u;
+      }
+      const int m = m0 + wm * WM + i * 16 + fr;
+      const int n = n0 + wn * (WN / 2) + j * 16 + 4 * fh;
+      *(uint2 *)(p.C + (size_t)m * p.ldc + n) = make_uint2(pack_bf16x2(h[0], h[1]),
+                                                           pack_bf16x2(h[2], h[3]));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j + 1 < TO; j += 2) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       float x[4], y[4];
@@ -832,7 +849,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
 //    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 (SDWA
 //    convert to fp32, v_cvt_pk_bf16_f32; |q| <= 127 is exact in bf16) one MFMA
 //    group before its MFMAs use it;
-//  * BN = 256 (waves 128 x 128) or 128 (waves 128 x 64); GATEUP pairs each
+//  * BN = 256 (waves 128 x 128), 192 (waves 128 x 96) or 128 (waves 128 x 64);
+//    GATEUP pairs each
 //    wave's WN/2 gate rows with the WN/2 up rows of the same output columns
 //    (blocks j and j + TN/2), as gemm_nt_kernel does;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
@@ -1406,6 +1424,14 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
     pl.wave4 = pl.bm == 256 && w4i8_ok;
+    if (pl.wave4) {
+      // 192 B rows (96 output columns) when that runs fewer columns per CU:
+      // rounds of 256 workgroups times columns per workgroup
+      const int64_t tm = (p.M + 255) / 256;
+      const int64_t r256 = (tm * ((p.N + 127) / 128) + 255) / 256;
+      const int64_t r192 = (tm * ((p.N + 95) / 96) + 255) / 256;
+      if (r192 * 96 < r256 * 128) pl.bn = 192;
+    }
     return pl;
   }
   if (w4i8_ok && p.M >= 256) {
@@ -1458,8 +1484,8 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.wave4) {
-      if (pl.bm != 256 || pl.bn != 256) return hipErrorInvalidValue;
-      return launch_w4i8<256, true>(p, stream);
+      if (pl.bm != 256 || (pl.bn != 256 && pl.bn != 192)) return hipErrorInvalidValue;
+      return pl.bn == 192 ? launch_w4i8<192, true>(p, stream) : launch_w4i8<256, true>(p, stream);
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
