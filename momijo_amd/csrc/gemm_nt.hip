@@ -891,6 +891,16 @@ __device__ __forceinline__ uint32_t i8x8_quarter(uint2 q, int p) {
   const float hi = (p & 1) ? (float)(v >> 24) : (float)((v << 16) >> 24);
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
+// The two halves of i8x8_quarter, so that the pack can be issued an MFMA
+// after the converts it consumes (their latency then hides under the MFMA).
+__device__ __forceinline__ void i8x8_quarter_cvt(uint2 q, int p, float &lo, float &hi) {
+  const int32_t v = (int32_t)(p < 2 ? q.x : q.y);
+  lo = (p & 1) ? (float)((v << 8) >> 24) : (float)((v << 24) >> 24);
+  hi = (p & 1) ? (float)(v >> 24) : (float)((v << 16) >> 24);
+}
+__device__ __forceinline__ uint32_t i8x8_quarter_pack(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
 
 __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 q) {
   const uint32_t w[2] = {q.x, q.y};
@@ -1011,7 +1021,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   bf16x8 fa[2][TM];
   uint2 fbr[2][TN];      // raw int8 B fragments
-  uint32_t fbc[2][4];    // widened B fragment (bf16x2 words) of this and the next group
+  // widened B fragments (bf16x2 words): group g of the kernel's sequence uses
+  // fbc[g % 3] while the fragment of group g + 2 is built in fbc[(g + 2) % 3]
+  uint32_t fbc[3][4];
+  float cvt_lo[4], cvt_hi[4];  // converted int8 pairs awaiting their pack
 
   constexpr int NDMA = A_DPW + B_DPW;
 #pragma unroll
@@ -1028,7 +1041,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) landed(fbr[0][j]);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) fbc[0][q] = i8x8_quarter(fbr[0][0], q);
+  for (int q = 0; q < 4; ++q) {
+    fbc[0][q] = i8x8_quarter(fbr[0][0], q);
+    fbc[1][q] = i8x8_quarter(fbr[0][TN > 1 ? 1 : 0], q);
+  }
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
 
   // one 32-deep step: MFMAs on fa[src] and the widened fbr[src]; the step's
@@ -1036,17 +1052,18 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   // B buffer bbuf and A buffer abuf) are spread over its groups, and its nload
   // direct loads (load_d, load_d + 1, ...) into buffer load_buf over its first
   // groups.  Group j widens the B fragment of group j + 1 (the last group: the
-  // next step's first, read at the start of this step) in four quarters of
-  // three VALU ops after its first four MFMAs, so the conversion hides under
-  // the MFMAs instead of stalling their issue, and four MFMAs separate the
-  // last VALU write from the first MFMA that reads it (the asm MFMAs are
-  // invisible to the compiler's hazard recognizer; that distance covers the
-  // VALU -> MFMA operand hazard).  Every index argument is a compile-time
+  // next step's first, read at the start of this step) in four quarters: the
+  // two converts of quarter u follow MFMA u and their pack follows MFMA u + 1,
+  // so the convert latency hides under an MFMA instead of stalling issue, and
+  // three MFMAs separate the last VALU write from the first MFMA that reads
+  // it (the asm MFMAs are invisible to the compiler's hazard recognizer; that
+  // distance covers the VALU -> MFMA operand hazard).  Every index argument is a compile-time
   // constant, so the fragment arrays stay in registers and the LDS pointers
   // keep their address space.
   auto step = [&](auto src_c, auto dst_c, auto abuf_c, auto bbuf_c, auto fast, int kt,
-                  auto load_d_c, auto nload_c, auto load_buf_c) {
+                  auto load_d_c, auto nload_c, auto load_buf_c, auto g0_c) {
     constexpr int src = decltype(src_c)::value, dst = decltype(dst_c)::value;
+    constexpr int g0 = decltype(g0_c)::value;  // sequence number of the step's group 0
     constexpr int abuf = decltype(abuf_c)::value, bbuf = decltype(bbuf_c)::value;
     constexpr int load_d = decltype(load_d_c)::value, nload = decltype(nload_c)::value;
     constexpr int load_buf = decltype(load_buf_c)::value;
@@ -1064,9 +1081,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
           else fa[dst][t - TN] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + (t - TN) * 16 * kBK);
         }
         __builtin_amdgcn_sched_barrier(0);
+        const int cur = (g0 + j) % 3, nxt = (g0 + j + 2) % 3;
         mfma_16x16x32_tied(acc[u][j],
-                           __builtin_bit_cast(bf16x8, make_uint4(fbc[j & 1][0], fbc[j & 1][1],
-                                                                 fbc[j & 1][2], fbc[j & 1][3])),
+                           __builtin_bit_cast(bf16x8, make_uint4(fbc[cur][0], fbc[cur][1],
+                                                                 fbc[cur][2], fbc[cur][3])),
                            fa[src][u]);
         if (u == 1 || u == 2) {
           // loads per group: ceil(nload / TN), the first at u = 1
@@ -1076,20 +1094,33 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
           if (u - 1 < lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (u < 4) {
+        {
+          // the fragment of group j + 2 (past the step's end: block
+          // j + 2 - TN of the next step, read at the start of this one):
+          // quarter q's two converts after MFMA 2q, its pack after MFMA 2q + 1
           __builtin_amdgcn_sched_barrier(0);
-          if (j + 1 < TN) {
-            fbc[(j + 1) & 1][u] = i8x8_quarter(fbr[src][j + 1], u);
+          const int q = u >> 1;
+          if (u & 1) {
+            fbc[nxt][q] = i8x8_quarter_pack(cvt_lo[q], cvt_hi[q]);
+          } else if (j + 2 < TN) {
+            i8x8_quarter_cvt(fbr[src][j + 2], q, cvt_lo[q], cvt_hi[q]);
           } else {
+            const int b = j + 2 - TN;
             if (u == 0) {
-              // fbr[dst][0] is this step's first read; the reads issued
-              // after it (t = 1 .. t0 of this group) may still be in flight
-              constexpr int kAfter = ((TN - 1) * NR + TN - 1) / TN;
-              static_assert(kAfter <= 15, "lgkmcnt field");
-              __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
-              landed(fbr[dst][0]);
+              // fbr[dst][b] is this step's read t = b; the t0 - b reads
+              // issued after it may still be in flight
+              if (j == TN - 2) {
+                constexpr int kAfter = ((TN - 2) * NR + TN - 1) / TN - 0;
+                static_assert(kAfter <= 15, "lgkmcnt field");
+                __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
+              } else {
+                constexpr int kAfter = ((TN - 1) * NR + TN - 1) / TN - 1;
+                static_assert(kAfter <= 15, "lgkmcnt field");
+                __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
+              }
+              landed(fbr[dst][b]);
             }
-            fbc[0][u] = i8x8_quarter(fbr[dst][0], u);
+            i8x8_quarter_cvt(fbr[dst][b], q, cvt_lo[q], cvt_hi[q]);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1097,12 +1128,13 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
     }
   };
   // stage kt in A buffer AB = (kt - kt0) % 2 and B buffer BB = (kt - kt0) % 3
-  auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
+  auto stage = [&](auto ab_c, auto bb_c, auto pos_c, auto fast, int kt) {
     constexpr int AB = decltype(ab_c)::value;
     constexpr int BB = decltype(bb_c)::value;
+    constexpr int G0 = decltype(pos_c)::value * 2 * TN;  // groups before this stage
     // step 0; loads of B for stage kt+2 go into B buffer (BB + 2) % 3
     step(IC<0>(), IC<1>(), IC<AB>(), IC<BB>(), fast, kt, IC<A_DPW>(), IC<B_DPW>(),
-         IC<(BB + 2) % 3>());
+         IC<(BB + 2) % 3>(), IC<G0 % 3>());
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
@@ -1112,7 +1144,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
     asm volatile("s_barrier" ::: "memory");
     // step 1; loads of A for stage kt+2 go into A buffer AB
     step(IC<1>(), IC<0>(), IC<AB ^ 1>(), IC<(BB + 1) % 3>(), fast, kt, IC<0>(), IC<A_DPW>(),
-         IC<AB>());
+         IC<AB>(), IC<(G0 + TN) % 3>());
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
@@ -1126,21 +1158,23 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   // stages kt .. kt+5 load stages kt+2 .. kt+7: fast while those lie inside K
   const int full_end = kt0 + (Kend - kt0 * kBK) / kBK;  // stages wholly inside the slice
   int kt = kt0;
+  // (the third argument is the stage's position in the 6-stage round, which
+  // fixes the rotation of the widened-fragment registers)
   for (; kt + 8 <= full_end; kt += 6) {
-    stage(I0(), I0(), F(), kt);
-    stage(I1(), I1(), F(), kt + 1);
-    stage(I0(), I2(), F(), kt + 2);
-    stage(I1(), I0(), F(), kt + 3);
-    stage(I0(), I1(), F(), kt + 4);
-    stage(I1(), I2(), F(), kt + 5);
+    stage(I0(), I0(), IC<0>(), F(), kt);
+    stage(I1(), I1(), IC<1>(), F(), kt + 1);
+    stage(I0(), I2(), IC<2>(), F(), kt + 2);
+    stage(I1(), I0(), IC<3>(), F(), kt + 3);
+    stage(I0(), I1(), IC<4>(), F(), kt + 4);
+    stage(I1(), I2(), IC<5>(), F(), kt + 5);
   }
   for (; kt < kt1; kt += 6) {
-    stage(I0(), I0(), S(), kt);
-    if (kt + 1 < kt1) stage(I1(), I1(), S(), kt + 1);
-    if (kt + 2 < kt1) stage(I0(), I2(), S(), kt + 2);
-    if (kt + 3 < kt1) stage(I1(), I0(), S(), kt + 3);
-    if (kt + 4 < kt1) stage(I0(), I1(), S(), kt + 4);
-    if (kt + 5 < kt1) stage(I1(), I2(), S(), kt + 5);
+    stage(I0(), I0(), IC<0>(), S(), kt);
+    if (kt + 1 < kt1) stage(I1(), I1(), IC<1>(), S(), kt + 1);
+    if (kt + 2 < kt1) stage(I0(), I2(), IC<2>(), S(), kt + 2);
+    if (kt + 3 < kt1) stage(I1(), I0(), IC<3>(), S(), kt + 3);
+    if (kt + 4 < kt1) stage(I0(), I1(), IC<4>(), S(), kt + 4);
+    if (kt + 5 < kt1) stage(I1(), I2(), IC<5>(), S(), kt + 5);
   }
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);
