@@ -218,7 +218,10 @@ def test_c4_prefill_gelu(oracle, dev):
     assert worst <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 64, 256), (100, 300, 1040), (257, 520, 512)])
+@pytest.mark.parametrize("M,N,K", [(9, 64, 256), (100, 300, 1040), (257, 520, 512),
+                                   # 256-row tiles with K % 64 != 0: a 2-way and a 4-way K
+                                   # split whose last slice ends inside a stage
+                                   (512, 384, 1040), (384, 1000, 2064)])
 def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M + N)
     lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_RELU)
@@ -255,7 +258,9 @@ def test_c5_mlp(oracle, dev):
     assert worst_h <= BF16_TOL and worst_y <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (40, 512, 256, 320), (300, 256, 528, 64)])
+@pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (40, 512, 256, 320), (300, 256, 528, 64),
+                                     # gate/up on 192-row tiles (a partial one), K % 64 != 0
+                                     (384, 1040, 400, 272)])
 def test_mlp_shapes(oracle, dev, M, K, I, H):
     case = _mlp_case(oracle, M, K, I, H, M)
     y, h = _run_mlp(dev, *case)
