@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import momijo_amd as mj
-from _util import bf16_dev, bf16_host_f32, normwise_rel, to_dev
+from _util import bf16_dev, bf16_host_bits, bf16_host_f32, normwise_rel, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -228,6 +228,26 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
     _, ref = oracle.linear_w8a16(x, Q, s, b, mj.EPI_RELU)
     assert normwise_rel(y, ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 256 x 128 tiles, one K slice
+                                   (512, 384, 1040),     # 2-way K split, partial last stage
+                                   (384, 1000, 2064)])   # 4-way K split, partial N tile
+def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
+    """Small-integer activations, int8 weights and power-of-two scales make
+    every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
+    in any order and under any K split, so the bf16 outputs (after scale,
+    bias and rounding) must equal the oracle's bit for bit; this pins every
+    tile, fragment and swizzle index of the 256-row W8A16 kernel."""
+    rng = np.random.default_rng(M + N + K)
+    x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, size=N)).astype(np.float32)
+    b = rng.integers(-8, 9, size=N).astype(np.float32) / np.float32(4)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_NONE)
+    y = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
+    ref, _ = oracle.linear_w8a16(x, Q, s, b, mj.EPI_NONE)
+    np.testing.assert_array_equal(y, ref)
 
 
 def _mlp_case(oracle, M, K, I, H, seed):
