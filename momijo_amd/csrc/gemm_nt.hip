@@ -846,13 +846,12 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
 //  * B rows are 64 bytes per stage in LDS, filled by direct loads (16 rows per
 //    1-KB load); the 16-byte chunk c of row r is stored at c ^ ((r >> 2) & 3);
 //  * a lane's B fragment of a 32-deep step is 8 int8 (one ds_read_b64 at
-//    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 (SDWA
-//    convert to fp32, v_cvt_pk_bf16_f32; |q| <= 127 is exact in bf16) one MFMA
-//    group before its MFMAs use it;
+//    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 in
+//    registers (i8x8_quarter: |q| <= 127 is exact in bf16) two MFMA groups
+//    before its MFMAs use it, at most two VALU ops beside each MFMA;
 //  * BN = 256 (waves 128 x 128), 192 (waves 128 x 96) or 128 (waves 128 x 64);
-//    GATEUP pairs each
-//    wave's WN/2 gate rows with the WN/2 up rows of the same output columns
-//    (blocks j and j + TN/2), as gemm_nt_kernel does;
+//    GATEUP pairs each wave's WN/2 gate rows with the WN/2 up rows of the same
+//    output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
 //    compiler put a full vmcnt(0) before each of them, which took away the
 //    load pipelining and doubled the kernel's time;
@@ -881,7 +880,8 @@ __device__ __forceinline__ uint2 ds_read8_asm(uint32_t addr) {
 // unrelated call.
 __device__ __forceinline__ void landed(uint2 &r) { asm volatile("" : "+v"(r)); }
 
-// Quarter p of i8x8_to_bf16x8: int8 2p and 2p+1 of the 8 in q as bf16x2.
+// Quarter p of an int8x8 fragment widened to bf16: int8 2p and 2p+1 of the
+// 8 in q as bf16x2.
 // An integer of magnitude <= 128 has at most 8 significant bits, so its bf16
 // is exactly the upper half of its fp32: one byte permute packs two (an
 // integer op, cheaper beside the MFMAs than the float convert-and-pack).
@@ -900,18 +900,6 @@ __device__ __forceinline__ void i8x8_quarter_cvt(uint2 q, int p, float &lo, floa
 }
 __device__ __forceinline__ uint32_t i8x8_quarter_pack(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-__device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 q) {
-  const uint32_t w[2] = {q.x, q.y};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int32_t v = (int32_t)w[i];
-    o[2 * i] = pack_bf16x2((float)((v << 24) >> 24), (float)((v << 16) >> 24));
-    o[2 * i + 1] = pack_bf16x2((float)((v << 8) >> 24), (float)(v >> 24));
-  }
-  return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
 template <int BN, bool GATEUP>
