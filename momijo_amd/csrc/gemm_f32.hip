@@ -2,10 +2,12 @@
 // Float32 and Float64 tensor engine (tensor/broadcast.mojo:1397-1900,
 // tensor/math.mojo:7838-7880, learn/nn/layers.mojo:383-433).
 //
-// gemm_fx_kernel<T>: C = epi(A @ B + bias) on v_mfma_f32_16x16x4f32 (T = float,
-// full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), 64x64 tile per
-// 256-thread workgroup, 16-wide K stages staged through LDS (k-major,
-// padded).  Operands come as (pointer, row stride, column stride), which
+// gemm_fx_kernel<T, TB>: C = epi(A @ B + bias) on v_mfma_f32_16x16x4f32 (T =
+// float, full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), a TB x TB
+// tile per 256-thread workgroup (64, or 128 for problems with enough tiles:
+// each wave then runs 4 x 4 MFMA blocks per LDS fragment read instead of
+// 2 x 2), 16-wide K stages staged through LDS (k-major, padded).  The tile
+// size does not change any output's summation order.  Operands come as (pointer, row stride, column stride), which
 // covers the reference's zero-copy transpose views; the loader walks
 // whichever dimension has unit stride with consecutive lanes so global reads
 // stay coalesced.  A grid dimension over broadcast batch indices serves
@@ -15,7 +17,7 @@
 
 namespace mj {
 
-constexpr int kFBM = 64, kFBN = 64, kFBK = 16;
+constexpr int kFBK = 16;
 
 typedef __attribute__((__vector_size__(4 * sizeof(double)))) double f64x4;
 
@@ -43,13 +45,17 @@ template <> struct Acc<double> {
 // value plus the finished product, one rounding).
 // The batch index (batch0 + blockIdx.y) is decomposed over up to 5 broadcast
 // batch dimensions into element offsets of A and B; C is contiguous per batch.
-template <typename T>
+template <typename T, int TB>
 __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const T *__restrict__ A,
                                                       int64_t sAm, int64_t sAk,
                                                       const T *__restrict__ B, int64_t sBk,
                                                       int64_t sBn, const T *__restrict__ bias,
                                                       int epi, int accum, T *__restrict__ C,
                                                       int64_t ldc, BatchDesc bd, int64_t batch0) {
+  constexpr int kFBM = TB, kFBN = TB;
+  constexpr int NB = TB / 32;   // 16 x 16 blocks per wave and dimension (waves 2 x 2)
+  constexpr int EPT = TB / 16;  // elements of each operand per thread per stage
+  constexpr int MF = 256 / TB;  // m-fast / n-fast loader: k rows per pass
   __shared__ T As[2][kFBK][kFBM + 4];
   __shared__ T Bs[2][kFBK][kFBN + 4];
 
@@ -78,20 +84,20 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   const bool a_k_fast = (sAk == 1);
   const bool b_n_fast = (sBn == 1) || (sBk != 1);
 
-  T ra[4], rb[4];
+  T ra[EPT], rb[EPT];
   auto load = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       int m, k;
       if (a_k_fast) { k = tid & 15; m = (tid >> 4) + 16 * i; }
-      else          { m = tid & 63; k = (tid >> 6) + 4 * i; }
+      else          { m = tid % TB; k = tid / TB + MF * i; }
       const int gm = m0 + m, gk = k0 + k;
       ra[i] = (gm < M && gk < K) ? A[(int64_t)gm * sAm + (int64_t)gk * sAk] : T(0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       int n, k;
-      if (b_n_fast) { n = tid & 63; k = (tid >> 6) + 4 * i; }
+      if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
       else          { k = tid & 15; n = (tid >> 4) + 16 * i; }
       const int gn = n0 + n, gk = k0 + k;
       rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : T(0);
@@ -99,26 +105,26 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       int m, k;
       if (a_k_fast) { k = tid & 15; m = (tid >> 4) + 16 * i; }
-      else          { m = tid & 63; k = (tid >> 6) + 4 * i; }
+      else          { m = tid % TB; k = tid / TB + MF * i; }
       As[buf][k][m] = ra[i];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       int n, k;
-      if (b_n_fast) { n = tid & 63; k = (tid >> 6) + 4 * i; }
+      if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
       else          { k = tid & 15; n = (tid >> 4) + 16 * i; }
       Bs[buf][k][n] = rb[i];
     }
   };
 
-  typename Acc<T>::V acc[2][2];
+  typename Acc<T>::V acc[NB][NB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < NB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
 
@@ -132,30 +138,30 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
     if (kt + 1 < nk) load((kt + 1) * kFBK);
 #pragma unroll
     for (int kk = 0; kk < kFBK; kk += 4) {
-      T a[2], b[2];
+      T a[NB], b[NB];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = As[buf][kk + fk][wm * 32 + i * 16 + fr];
+      for (int i = 0; i < NB; ++i) a[i] = As[buf][kk + fk][wm * (TB / 2) + i * 16 + fr];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = Bs[buf][kk + fk][wn * 32 + j * 16 + fr];
+      for (int j = 0; j < NB; ++j) b[j] = Bs[buf][kk + fk][wn * (TB / 2) + j * 16 + fr];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Acc<T>::mfma(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < NB; ++j) acc[i][j] = Acc<T>::mfma(a[i], b[j], acc[i][j]);
     }
     if (kt + 1 < nk) store(buf ^ 1);
     __syncthreads();
   }
 
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+  for (int j = 0; j < NB; ++j) {
+    const int n = n0 + wn * (TB / 2) + j * 16 + (lane & 15);
     if (n >= N) continue;
     const T bb = bias ? bias[n] : T(0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 32 + i * 16 + Acc<T>::row(lane, r);
+        const int m = m0 + wm * (TB / 2) + i * 16 + Acc<T>::row(lane, r);
         if (m < M) {
           T v = acc[i][j][r];
           if (bias) {
@@ -179,15 +185,26 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
                             int64_t sAk, const T *B, int64_t sBk, int64_t sBn, const T *bias,
                             int epi, int accum, T *C, int64_t ldc, const BatchDesc &bd,
                             int64_t batches, hipStream_t stream) {
-  const int64_t tiles64 = ((M + kFBM - 1) / kFBM) * ((N + kFBN - 1) / kFBN);
+  // 128 x 128 tiles for matrices of at least 256 x 256 once they still give
+  // every CU two workgroups; smaller problems keep 64 x 64 (more workgroups
+  // for the latency, less padding for small batched matrices)
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+  const bool big = M >= 256 && N >= 256 && tiles128 * batches >= 512;
+  const int TBs = big ? 128 : 64;
+  const int64_t tiles64 = ((M + TBs - 1) / TBs) * ((N + TBs - 1) / TBs);
   if (tiles64 > INT32_MAX) return hipErrorInvalidValue;  // grid.x limit
   const int tiles = (int)tiles64;
   constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < batches; b0 += kMaxGridY) {
     const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;
-    hipLaunchKernelGGL(gemm_fx_kernel<T>, dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
-                       (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C, ldc,
-                       bd, b0);
+    if (big)
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 128>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
+                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
+                         ldc, bd, b0);
+    else
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 64>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
+                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
+                         ldc, bd, b0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

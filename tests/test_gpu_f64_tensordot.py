@@ -45,6 +45,20 @@ def test_f64_integer_exact(oracle, dev):
     np.testing.assert_array_equal(_mm64(A, B, dev), oracle.matmul_f64(A, B))
 
 
+@pytest.mark.parametrize("tb", [False, True])
+def test_f64_large_tiles_integer_exact(oracle, dev, tb):
+    """3000 x 2900 outputs on the 128 x 128 fp64 tile: integer operands
+    below 2^20 keep every sum exact (|sum| < 2^53), so bit-identical."""
+    rng = np.random.default_rng(13 + tb)
+    M, N, K = 3000, 2900, 40
+    A = rng.integers(-2**20, 2**20, size=(M, K)).astype(np.float64)
+    B = rng.integers(-2**20, 2**20, size=(K, N)).astype(np.float64)
+    b = mj.Tensor(to_dev(B, dev)) if not tb else \
+        mj.Tensor(to_dev(np.ascontiguousarray(B.T), dev)).transpose()
+    got = mj.matmul(mj.Tensor(to_dev(A, dev)), b).numpy()
+    np.testing.assert_array_equal(got, oracle.matmul_f64(A, B))
+
+
 def test_f64_transposed_views(oracle, dev):
     rng = np.random.default_rng(12)
     x = rng.standard_normal((40, 75))

@@ -45,6 +45,28 @@ def test_matmul_integer_inputs_exact(oracle, dev):
     np.testing.assert_array_equal(got, oracle.matmul_f32(A, B))
 
 
+def _view(M, dev, transposed):
+    """M as a device Tensor, either contiguous or as the transpose view of
+    its contiguous transpose (same values, swapped strides)."""
+    if not transposed:
+        return mj.Tensor(to_dev(M, dev))
+    return mj.Tensor(to_dev(np.ascontiguousarray(M.T), dev)).transpose()
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True)])
+def test_matmul_large_tiles_integer_exact(oracle, dev, ta, tb):
+    """A 3000 x 2900 product runs on 128 x 128 tiles (smaller ones on
+    64 x 64); small-integer operands make every sum exact, so the result is
+    bit-identical to the oracle, also through transposed views (both loader
+    orientations of A and of B)."""
+    rng = np.random.default_rng(7 + 2 * ta + tb)
+    M, N, K = 3000, 2900, 72
+    A = rng.integers(-8, 9, size=(M, K)).astype(np.float32)
+    B = rng.integers(-8, 9, size=(K, N)).astype(np.float32)
+    got = mj.matmul(_view(A, dev, ta), _view(B, dev, tb)).numpy()
+    np.testing.assert_array_equal(got, oracle.matmul_f32(A, B))
+
+
 def test_matmul_transposed_views(oracle, dev):
     """x.matmul(W.transpose()) and A.transpose().matmul(B) run on the stride
     views, as the reference's strided path does (broadcast.mojo:1647-1673)."""
