@@ -4,9 +4,10 @@
 //
 // gemm_fx_kernel<T, TB>: C = epi(A @ B + bias) on v_mfma_f32_16x16x4f32 (T =
 // float, full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), a TB x TB
-// tile per 256-thread workgroup (64, or 128 for problems with enough tiles:
+// tile per 256-thread workgroup (64; 128 for problems with enough tiles, where
 // each wave then runs 4 x 4 MFMA blocks per LDS fragment read instead of
-// 2 x 2), 16-wide K stages staged through LDS (k-major, padded).  The tile
+// 2 x 2; 32 for tiny latency-bound problems, one block per wave), 16-wide K
+// stages staged through LDS (k-major, padded).  The tile
 // size does not change any output's summation order.  Operands come as (pointer, row stride, column stride), which
 // covers the reference's zero-copy transpose views; the loader walks
 // whichever dimension has unit stride with consecutive lanes so global reads
@@ -186,11 +187,14 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
                             int epi, int accum, T *C, int64_t ldc, const BatchDesc &bd,
                             int64_t batches, hipStream_t stream) {
   // 128 x 128 tiles for matrices of at least 256 x 256 once they still give
-  // every CU two workgroups; smaller problems keep 64 x 64 (more workgroups
-  // for the latency, less padding for small batched matrices)
+  // every CU two workgroups; problems of fewer than 64 tiles of 64 x 64 take
+  // 32 x 32 tiles (a latency-bound launch: a quarter of the MFMA chain per
+  // wave and four times the workgroups; 256^3 Linear 17.4 -> 8.4 us); the
+  // rest 64 x 64
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool big = M >= 256 && N >= 256 && tiles128 * batches >= 512;
-  const int TBs = big ? 128 : 64;
+  const bool tiny = !big && ((M + 63) / 64) * ((N + 63) / 64) * batches < 64;
+  const int TBs = big ? 128 : (tiny ? 32 : 64);
   const int64_t tiles64 = ((M + TBs - 1) / TBs) * ((N + TBs - 1) / TBs);
   if (tiles64 > INT32_MAX) return hipErrorInvalidValue;  // grid.x limit
   const int tiles = (int)tiles64;
@@ -199,6 +203,10 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
     const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;
     if (big)
       hipLaunchKernelGGL((gemm_fx_kernel<T, 128>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
+                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
+                         ldc, bd, b0);
+    else if (tiny)
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 32>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
                          ldc, bd, b0);
     else
