@@ -486,7 +486,7 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
   if (!y || !scales || (K > 0 && (!x || !Q))) return fail(MJ_ERR_ARG, "null operand");
   if (K % 16 || !aligned16(x) || !aligned16(Q))
     return fail(MJ_ERR_UNSUPPORTED, "W8A16 Linear needs K %% 16 == 0 and 16-byte aligned x, Q");
-  if (M <= 8)
+  if (M <= mj::kGemvMaxM)
     return hip_status(mj::launch_gemv_w8a16(x, Q, scales, bias, epilogue, y, M, N, K, S(stream)),
                       "gemv_w8a16 launch");
   mj::GemmNT p;
@@ -510,7 +510,7 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   gu.A = x; gu.lda = K; gu.B = Wg; gu.B2 = Wu; gu.ldb = K; gu.scales = sg; gu.scales2 = su;
   gu.C = h; gu.ldc = I; gu.M = M; gu.N = I; gu.K = K; gu.bkind = mj::B_INT8; gu.gate_up = true;
   if (int32_t st = run_gemm_nt(gu, S(stream), "gate/up")) return st;
-  if (M <= 8)
+  if (M <= mj::kGemvMaxM)
     return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
                                             S(stream)),
                       "down gemv launch");

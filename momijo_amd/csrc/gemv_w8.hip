@@ -153,6 +153,107 @@ __global__ __launch_bounds__(256) void gemv_w8a16_kernel(const uint16_t *__restr
   }
 }
 
+// Skinny-M W8A16 GEMV on MFMA (3 <= M <= 16): with several x rows the
+// per-lane multiply-adds (M per weight) make the VALU kernel above compute
+// bound, so here the products go to v_mfma_f32_16x16x32_bf16 and the lanes
+// only widen the weights (int8 -> bf16, exact).  A workgroup owns 16 weight
+// rows; its KQ waves take consecutive parts of K, and their
+// 16 x 16 fp32 partial tiles are added in part order through LDS (a fixed
+// order: deterministic).  Per 64-deep K block a lane loads 16 int8 of one
+// weight row (row lane % 16, k chunk lane / 16: 1 KB per load, 64 bytes per
+// row) and 2 x 16 bytes of the same k range of x row lane % 16 (rows past M
+// read zero); the first 8 k of the chunk feed the block's first MFMA and the
+// other 8 the second, for weights and x alike, so each MFMA still sums
+// matching k.  Loads run four blocks ahead through a register ring.
+__device__ __forceinline__ bf16x8 i8x8_bf16(uint32_t lo, uint32_t hi) {
+  uint32_t o[4];
+  const uint32_t w[2] = {lo, hi};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int32_t v = (int32_t)w[i];
+    o[2 * i] = __builtin_amdgcn_perm(__float_as_uint((float)((v << 16) >> 24)),
+                                     __float_as_uint((float)((v << 24) >> 24)), 0x07060302u);
+    o[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint((float)(v >> 24)),
+                                         __float_as_uint((float)((v << 8) >> 24)), 0x07060302u);
+  }
+  return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+template <int KQ>  // waves per workgroup, each a consecutive 1/KQ of K
+__global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t *__restrict__ x,
+                                                              const int8_t *__restrict__ Q,
+                                                              const float *__restrict__ scales,
+                                                              const float *__restrict__ bias,
+                                                              int epi, uint16_t *__restrict__ y,
+                                                              int M, int N, int K) {
+  __shared__ f32x4 red[KQ][64];
+  constexpr int D = 4;  // blocks in flight per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int r = lane & 15, c = lane >> 4;
+  const int rows = N - n0 < 16 ? N - n0 : 16;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
+  const int nblk = (K + 63) / 64;
+  const int per = (nblk + KQ - 1) / KQ;
+  const int b0 = wave * per;
+  const int b1 = b0 + per < nblk ? b0 + per : nblk;
+  const bool xrow = r < M;
+  uint4 qw[D], xa[D], xb[D];
+  auto issue = [&](int b, int slot) {
+    const int k = b * 64 + c * 16;
+    const bool ok = b < b1 && k < K;
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+        rQ, ok ? (uint32_t)(r * K + k) : kOobOffset, 0, 2 /* nt */);
+    qw[slot] = make_uint4(v[0], v[1], v[2], v[3]);
+    if (xrow) {  // lanes of x rows past M keep zeros
+      const uint32_t xo = ok ? (uint32_t)((r * K + k) * 2) : kOobOffset;
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+      const u32x4 bb = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+      xa[slot] = make_uint4(a[0], a[1], a[2], a[3]);
+      xb[slot] = make_uint4(bb[0], bb[1], bb[2], bb[3]);
+    }
+  };
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int d = 0; d < D; ++d) xa[d] = xb[d] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(b0 + d, d);
+  for (int b = b0; b < b1; b += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (b + d < b1) {
+        const bf16x8 w0 = i8x8_bf16(qw[d].x, qw[d].y), w1 = i8x8_bf16(qw[d].z, qw[d].w);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(bf16x8, xa[d]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(bf16x8, xb[d]), acc, 0, 0, 0);
+        issue(b + d + D, d);
+      }
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int w = 0; w < KQ; ++w) sum += red[w][lane];
+  // lane: x row m = lane % 16, weight rows n0 + 4 (lane / 16) + q
+  const int m = r;
+  if (m >= M) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = n0 + 4 * c + q;
+    if (n >= N) break;
+    float v;
+    {
+#pragma clang fp contract(off)
+      v = sum[q] * scales[n];
+      if (bias) v = v + bias[n];
+    }
+    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi(epi, v));
+  }
+}
+
 template <int MB>
 static hipError_t launch_mb(const uint16_t *x, const int8_t *Q, const float *scales,
                             const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
@@ -172,13 +273,27 @@ static hipError_t launch_mb(const uint16_t *x, const int8_t *Q, const float *sca
   return hipGetLastError();
 }
 
+// x rows from which the MFMA kernel takes the GEMV.  11008 x 4096 on MI355X
+// (graph replay, weights rotated past the MALL): M = 2 13.3 us VALU against
+// 15.2 MFMA; M = 3 18.7 / 15.6; M = 4 21.4 / 16.1; M = 8 35.0 / 17.9.  With
+// 8 waves per workgroup (K in eighths) or 8 blocks in flight per wave the
+// MFMA kernel measured 1-2 us slower.
+constexpr int kGemvMfmaMinM = 3;
+
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream) {
+  if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
+    // 32-bit buffer offsets over the x rows and the 16 weight rows of a workgroup
+    if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 16 * K >= ((int64_t)1 << 31))
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemv_w8a16_mfma_kernel<4>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0,
+                       stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+    return hipGetLastError();
+  }
   if (M <= 1) return launch_mb<1>(x, Q, scales, bias, epi, y, M, N, K, stream);
   if (M <= 2) return launch_mb<2>(x, Q, scales, bias, epi, y, M, N, K, stream);
-  if (M <= 4) return launch_mb<4>(x, Q, scales, bias, epi, y, M, N, K, stream);
-  return launch_mb<8>(x, Q, scales, bias, epi, y, M, N, K, stream);
+  return hipErrorInvalidValue;  // M > kGemvMaxM is the GEMM's
 }
 
 }  // namespace mj

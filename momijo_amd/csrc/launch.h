@@ -80,6 +80,10 @@ hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,
                                  hipStream_t stream);
 
 // ---- gemv_w8.hip: skinny-M W8A16 -----------------------------------------
+// Largest x row count the W8A16 GEMV kernels take; larger M runs the int8
+// MFMA GEMM (at M = 9..16 the GEMV's MFMA kernel takes 18-22 us on
+// 11008 x 4096 where the 256-row GEMM tile takes 38 us).
+constexpr int64_t kGemvMaxM = 16;
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream);

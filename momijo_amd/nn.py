@@ -129,8 +129,9 @@ class W8Linear:
     per-channel generalisation of QuantLinear's weights, applied to the
     reference's Linear layout [OutF, InF].
 
-    y = bf16(epi((x . q^T) * scale[n] + bias[n])); M <= 8 rows take the
-    streaming GEMV kernel, more rows the MFMA GEMM."""
+    y = bf16(epi((x . q^T) * scale[n] + bias[n])); M <= 16 rows take the
+    GEMV kernels (streaming for M <= 2, skinny MFMA above), more rows the
+    MFMA GEMM."""
 
     def __init__(self, q: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None,
                  epi: int = _lib.EPI_NONE):

@@ -76,12 +76,13 @@ def _w8(oracle, M, N, K, seed):
     return x, Q, s, b
 
 
-@pytest.mark.parametrize("M", [8, 9])
+@pytest.mark.parametrize("M", [2, 3, 16, 17])
 @pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU, mj.EPI_GELU_TANH, mj.EPI_SILU,
                                  mj.EPI_GELU_TANH_APPROX, mj.EPI_SILU_APPROX,
                                  mj.EPI_RELU_UNARY])
 def test_w8a16_gemv_gemm_switch_every_epilogue(oracle, dev, M, epi):
-    """M = 8 is the last GEMV size, M = 9 the first MFMA GEMM size."""
+    """M = 2 is the last streaming-GEMV size, M = 3 the first skinny-MFMA GEMV
+    size, M = 16 its last and M = 17 the first MFMA GEMM size."""
     x, Q, s, b = _w8(oracle, M, 192, 512, M * 10 + epi)
     lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), epi)
     y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))

@@ -193,8 +193,8 @@ def test_c3_gemv(oracle, dev):
     assert err <= BF16_TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16])
+@pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16), (17, 48)])
 def test_gemv_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M * 100 + N)
     for bias, epi in ((b, mj.EPI_NONE), (None, mj.EPI_GELU_TANH), (b, mj.EPI_SILU)):
@@ -218,7 +218,7 @@ def test_c4_prefill_gelu(oracle, dev):
     assert worst <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 64, 256), (100, 300, 1040), (257, 520, 512),
+@pytest.mark.parametrize("M,N,K", [(17, 64, 256), (100, 300, 1040), (257, 520, 512),
                                    # 256-row tiles with K % 64 != 0: a 2-way and a 4-way K
                                    # split whose last slice ends inside a stage
                                    (512, 384, 1040), (384, 1000, 2064)])
@@ -232,13 +232,18 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 256 x 128 tiles, one K slice
                                    (512, 384, 1040),     # 2-way K split, partial last stage
-                                   (384, 1000, 2064)])   # 4-way K split, partial N tile
+                                   (384, 1000, 2064),    # 4-way K split, partial N tile
+                                   # skinny-M MFMA GEMV: partial 16-row tile of
+                                   # weights, K % 64 != 0, x rows < 16
+                                   (3, 4104, 1040), (16, 1000, 4096),
+                                   (7, 37, 80)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
     in any order and under any K split, so the bf16 outputs (after scale,
     bias and rounding) must equal the oracle's bit for bit; this pins every
-    tile, fragment and swizzle index of the 256-row W8A16 kernel."""
+    tile, fragment and swizzle index of the 256-row W8A16 kernel and of the
+    skinny-M MFMA GEMV."""
     rng = np.random.default_rng(M + N + K)
     x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
     Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
@@ -278,7 +283,7 @@ def test_c5_mlp(oracle, dev):
     assert worst_h <= BF16_TOL and worst_y <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (40, 512, 256, 320), (300, 256, 528, 64),
+@pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (12, 256, 400, 130), (40, 512, 256, 320), (300, 256, 528, 64),
                                      # gate/up on 192-row tiles (a partial one), K % 64 != 0
                                      (384, 1040, 400, 272)])
 def test_mlp_shapes(oracle, dev, M, K, I, H):
