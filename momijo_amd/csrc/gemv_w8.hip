@@ -1,7 +1,8 @@
 // Skinny-M W8A16 Linear (decode): y[m,n] = bf16(epi((x[m,:] . Q[n,:]) *
-// scales[n] + bias[n])) for M <= 8, int8 weights Q [N,K] streamed once.
+// scales[n] + bias[n])) for M <= 16, int8 weights Q [N,K] streamed once:
+// the streaming kernel below for M <= 2, the MFMA kernel after it above.
 //
-// The kernel is HBM-bound (1 byte of weight per multiply-add), so the design
+// The streaming kernel is HBM-bound (1 byte of weight per multiply-add), so the design
 // goal is bytes in flight: each wave owns RPW consecutive weight rows and
 // issues all of its 16-byte weight loads for a K block before doing any math;
 // lane l covers K chunks l, l+64, ... of 16 int8, so a wave reads 1 KiB
