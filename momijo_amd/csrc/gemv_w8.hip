@@ -180,20 +180,24 @@ __device__ __forceinline__ bf16x8 i8x8_bf16(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int KQ>  // waves per workgroup, each a consecutive 1/KQ of K
+// KQ waves per workgroup, each a consecutive 1/KQ of K; RT tiles of 16 weight
+// rows per workgroup, which share each x fragment (x is read once per 16*RT
+// weight rows; wave t < RT finishes tile t)
+template <int KQ, int RT>
 __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t *__restrict__ x,
                                                               const int8_t *__restrict__ Q,
                                                               const float *__restrict__ scales,
                                                               const float *__restrict__ bias,
                                                               int epi, uint16_t *__restrict__ y,
                                                               int M, int N, int K) {
-  __shared__ f32x4 red[KQ][64];
+  static_assert(RT <= KQ, "one finishing wave per row tile");
+  __shared__ f32x4 red[KQ][RT][64];
   constexpr int D = 4;  // blocks in flight per wave
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * RT;
   const int r = lane & 15, c = lane >> 4;
-  const int rows = N - n0 < 16 ? N - n0 : 16;
+  const int rows = N - n0 < 16 * RT ? N - n0 : 16 * RT;
   const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
   const int nblk = (K + 63) / 64;
@@ -201,13 +205,16 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
   const int b0 = wave * per;
   const int b1 = b0 + per < nblk ? b0 + per : nblk;
   const bool xrow = r < M;
-  uint4 qw[D], xa[D], xb[D];
+  uint4 qw[D][RT], xa[D], xb[D];
   auto issue = [&](int b, int slot) {
     const int k = b * 64 + c * 16;
     const bool ok = b < b1 && k < K;
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-        rQ, ok ? (uint32_t)(r * K + k) : kOobOffset, 0, 2 /* nt */);
-    qw[slot] = make_uint4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {  // rows past the tile read zero (buffer bounds)
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+          rQ, ok ? (uint32_t)((t * 16 + r) * K + k) : kOobOffset, 0, 2 /* nt */);
+      qw[slot][t] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
     if (xrow) {  // lanes of x rows past M keep zeros
       const uint32_t xo = ok ? (uint32_t)((r * K + k) * 2) : kOobOffset;
       const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
@@ -216,7 +223,9 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
       xb[slot] = make_uint4(bb[0], bb[1], bb[2], bb[3]);
     }
   };
-  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int d = 0; d < D; ++d) xa[d] = xb[d] = make_uint4(0, 0, 0, 0);
 #pragma unroll
@@ -225,25 +234,32 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       if (b + d < b1) {
-        const bf16x8 w0 = i8x8_bf16(qw[d].x, qw[d].y), w1 = i8x8_bf16(qw[d].z, qw[d].w);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(bf16x8, xa[d]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(bf16x8, xb[d]), acc, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          const bf16x8 w0 = i8x8_bf16(qw[d][t].x, qw[d][t].y);
+          const bf16x8 w1 = i8x8_bf16(qw[d][t].z, qw[d][t].w);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(bf16x8, xa[d]),
+                                                           acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(bf16x8, xb[d]),
+                                                           acc[t], 0, 0, 0);
+        }
         issue(b + d + D, d);
       }
     }
   }
-  red[wave][lane] = acc;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) red[wave][t][lane] = acc[t];
   __syncthreads();
-  if (wave != 0) return;
+  if (wave >= RT) return;
   f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int w = 0; w < KQ; ++w) sum += red[w][lane];
-  // lane: x row m = lane % 16, weight rows n0 + 4 (lane / 16) + q
+  for (int w = 0; w < KQ; ++w) sum += red[w][wave][lane];
+  // lane: x row m = lane % 16, weight rows n0 + 16 wave + 4 (lane / 16) + q
   const int m = r;
   if (m >= M) return;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int n = n0 + 4 * c + q;
+    const int n = n0 + 16 * wave + 4 * c + q;
     if (n >= N) break;
     float v;
     {
@@ -285,11 +301,17 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream) {
   if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
-    // 32-bit buffer offsets over the x rows and the 16 weight rows of a workgroup
-    if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 16 * K >= ((int64_t)1 << 31))
+    // 32-bit buffer offsets over the x rows and the 64 weight rows of a workgroup
+    if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 64 * K >= ((int64_t)1 << 31))
       return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemv_w8a16_mfma_kernel<4>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0,
-                       stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+    if (M > 8)  // 4 row tiles: M = 16 22.0 -> 19.4 us; slower at M <= 4 (15.4 -> 17.5)
+      hipLaunchKernelGGL((gemv_w8a16_mfma_kernel<4, 4>), dim3((unsigned)((N + 63) / 64)),
+                         dim3(256), 0, stream, x, Q, scales, bias, epi, y, (int)M, (int)N,
+                         (int)K);
+    else
+      hipLaunchKernelGGL((gemv_w8a16_mfma_kernel<4, 1>), dim3((unsigned)((N + 15) / 16)),
+                         dim3(256), 0, stream, x, Q, scales, bias, epi, y, (int)M, (int)N,
+                         (int)K);
     return hipGetLastError();
   }
   if (M <= 1) return launch_mb<1>(x, Q, scales, bias, epi, y, M, N, K, stream);
