@@ -249,7 +249,8 @@ def bench_c4(steps, warmup):
         "metric": "W8A16 GEMM + bias + GELU TFLOP/s",
         "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                     "traffic": _traffic("c4_w8a16_prefill_gelu_2048x4096x4096")},
     }
 
 
@@ -272,7 +273,8 @@ def bench_c5(steps, warmup):
         "metric": "W8A16 Llama FFN TFLOP/s (gate/up + down)",
         "value": tf, "unit": "TFLOP/s", "ms_per_step": ms,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                     "traffic": _traffic("c5_w8a16_mlp_512x4096x11008")},
     }
 
 
