@@ -149,6 +149,38 @@ __device__ __forceinline__ float apply_epi(int epi, float v) {
   }
 }
 
+// GELU (tanh form) and SiLU for results that are rounded to bf16 (the bf16
+// and W8A16 GEMM/GEMV epilogues).  0.5 x (1 + tanh t) = x * sigmoid(2t), so
+// gelu = x / (1 + 2^(-2 t log2 e)) and silu = x / (1 + 2^(-x log2 e)), with
+// the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each).
+// The relative error is a few 1e-6 (mostly the rounding of the exponent's
+// argument), so the bf16 result equals that of gelu32 / silu32 except within
+// about 1e-6 of a bf16 rounding boundary, and except GELU at x < -2: there
+// gelu32's 1 + tanh(t) cancels and loses more than a bf16 step of its tiny
+// result (|gelu| < 0.05, absolute error < 1e-6), which this form does not.
+// Limits as gelu32 / silu32: +inf
+// -> +inf, -inf -> NaN, large negative x -> -0, NaN -> NaN.  It costs about
+// a quarter of the VALU cycles of the expf + IEEE division forms, which a
+// GEMM epilogue spends with nothing left to overlap (C4: 128 GELUs per lane,
+// 16 us of a 71 us launch before this form).
+__device__ __forceinline__ float gelu_b16(float x) {
+  const float a = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 k log2(e)
+  const float u = x + 0.044715f * (x * x * x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * u));
+}
+
+__device__ __forceinline__ float silu_b16(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+__device__ __forceinline__ float apply_epi_b16(int epi, float v) {
+  switch (epi) {
+    case EPI_GELU_TANH: return gelu_b16(v);
+    case EPI_SILU: return silu_b16(v);
+    default: return apply_epi(epi, v);
+  }
+}
+
 // ---------------------------------------------------------------- reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -32,7 +32,7 @@
 //  * gate/up mode (Llama FFN): each wave's B rows are WN/2 gate rows then the
 //    WN/2 up rows of the same output columns, so block j (gate) and block
 //    j + TN/2 (up) of a lane hold g and u for the same (m, n), and the lane
-//    writes silu32(g*sg) * (u*su) directly;
+//    writes silu(g*sg) * (u*su) directly;
 //  * split-K (when the tile grid alone cannot fill the 256 CUs): workgroup
 //    (split, tile) accumulates its K slice into an fp32 partial buffer and a
 //    second kernel sums the partials in split order and applies the epilogue.
@@ -154,7 +154,7 @@ __device__ __forceinline__ void stage_tile(const GemmNT &p, const f32x4 (&acc)[T
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        v[q] = apply_epi(E, epi_scale_bias(acc[i][j][q], s[q], b[q], has_s, has_b));
+        v[q] = apply_epi_b16(E, epi_scale_bias(acc[i][j][q], s[q], b[q], has_s, has_b));
       *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(v[0], v[1]),
                                                  pack_bf16x2(v[2], v[3]));
     }
@@ -163,7 +163,7 @@ __device__ __forceinline__ void stage_tile(const GemmNT &p, const f32x4 (&acc)[T
 
 // Gate/up epilogue into the staging tile: blocks j < TN/2 are the gate,
 // blocks j + TN/2 the up projection of the same output columns;
-// h = silu32(g*sg) * (u*su).
+// h = silu(g*sg) * (u*su) (silu_b16).
 template <int TM, int TN, int WM, int WN, int BN_OUT>
 __device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x4 (&acc)[TM][TN],
                                              uint16_t *ct, int n0, int wm, int wn, int lane) {
@@ -189,7 +189,7 @@ __device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x4 (&acc)
         const float uv = epi_scale_bias(acc[i][j + TN / 2][q], su[q], 0.0f, true, false);
         {
 #pragma clang fp contract(off)
-          h[q] = silu32(gv) * uv;
+          h[q] = silu_b16(gv) * uv;
         }
       }
       *(uint2 *)(ct + ml * LD + nl) = make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
@@ -553,8 +553,8 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
       float x[4], y[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        x[q] = apply_epi(E, epi_scale_bias(acc[i][j][q], s0[q], b0[q], has_s, has_b));
-        y[q] = apply_epi(E, epi_scale_bias(acc[i][j + 1][q], s1[q], b1[q], has_s, has_b));
+        x[q] = apply_epi_b16(E, epi_scale_bias(acc[i][j][q], s0[q], b0[q], has_s, has_b));
+        y[q] = apply_epi_b16(E, epi_scale_bias(acc[i][j + 1][q], s1[q], b1[q], has_s, has_b));
       }
       const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
                                                        pack_bf16x2(y[0], y[1]), false, false);
@@ -568,7 +568,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
 }
 
 // Gate/up epilogue of a full, aligned tile straight from the accumulators:
-// h = silu32(g*sg) * (u*su) for blocks j < TN/2 (gate) and j + TN/2 (up),
+// h = silu(g*sg) * (u*su) (silu_b16) for blocks j < TN/2 (gate) and j + TN/2 (up),
 // then the same permlane pairing as store_tile_direct over the TN/2 output
 // blocks; an odd last block is stored 8 bytes (4 columns) per lane.
 template <int TM, int TN, int WM, int WN>
@@ -595,7 +595,7 @@ __device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4
 #pragma clang fp contract(off)
         const float g = epi_scale_bias(acc[i][j][q], sg[j][q], 0.0f, true, false);
         const float u = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
-        h[q] = silu32(g) * u;
+        h[q] = silu_b16(g) * u;
       }
       const int m = m0 + wm * WM + i * 16 + fr;
       const int n = n0 + wn * (WN / 2) + j * 16 + 4 * fh;
@@ -615,8 +615,8 @@ __device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4
         const float u0 = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
         const float g1 = epi_scale_bias(acc[i][j + 1][q], sg[j + 1][q], 0.0f, true, false);
         const float u1 = epi_scale_bias(acc[i][j + 1 + TO][q], su[j + 1][q], 0.0f, true, false);
-        x[q] = silu32(g0) * u0;
-        y[q] = silu32(g1) * u1;
+        x[q] = silu_b16(g0) * u0;
+        y[q] = silu_b16(g1) * u1;
       }
       const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
                                                        pack_bf16x2(y[0], y[1]), false, false);
@@ -1245,7 +1245,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
 #pragma unroll
         for (int sp = 0; sp < 8; ++sp)
           if (sp < p.splits) acc += part[sp][q >> 2][q & 3];
-        v[q] = apply_epi(E, epi_scale_bias(acc, has_s ? p.scales[nb + q] : 1.0f,
+        v[q] = apply_epi_b16(E, epi_scale_bias(acc, has_s ? p.scales[nb + q] : 1.0f,
                                            has_b ? p.bias[nb + q] : 0.0f, has_s, has_b));
       }
       *(uint4 *)(p.C + (size_t)m * p.ldc + nb) =
@@ -1266,7 +1266,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
       const int n = nb + q < N ? nb + q : N - 1;
       float acc = 0.0f;
       for (int s = 0; s < p.splits; ++s) acc += p.part[s * plane + (size_t)m * N + n];
-      v[q] = apply_epi(E, epi_scale_bias(acc, has_s ? p.scales[n] : 1.0f,
+      v[q] = apply_epi_b16(E, epi_scale_bias(acc, has_s ? p.scales[n] : 1.0f,
                                          has_b ? p.bias[n] : 0.0f, has_s, has_b));
     }
     store4_bf16(p, m, nb, v);

@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void gemv_w8a16_kernel(const uint16_t *__restr
           v = s * my_s;
           if (bias) v = v + my_b;
         }
-        v = apply_epi(epi, v);
+        v = apply_epi_b16(epi, v);
         y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
       }
     }
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
       v = sum[q] * scales[n];
       if (bias) v = v + bias[n];
     }
-    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi(epi, v));
+    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
   }
 }
 

@@ -255,6 +255,44 @@ def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     np.testing.assert_array_equal(y, ref)
 
 
+@pytest.mark.parametrize("M", [1, 5, 12, 40, 256])
+@pytest.mark.parametrize("epi", [mj.EPI_GELU_TANH, mj.EPI_SILU])
+def test_w8a16_gelu_silu_epilogue_exact_sums(oracle, dev, M, epi):
+    """The bf16-output epilogues evaluate GELU as x / (1 + 2^(-2t log2 e))
+    and SiLU as x / (1 + 2^(-x log2 e)) with the hardware exp2 and
+    reciprocal, where the oracle follows the reference's literal expf and
+    division forms.  With integer inputs the sums are exact, so the only
+    difference left is the activation itself: every bf16 output is within one
+    bf16 step (2^-7 relative) of the oracle's fp32 value before rounding, or
+    within 1e-6 absolute.  For GELU at x < -2 the literal form's 1 + tanh(t)
+    cancels (its own error there exceeds a bf16 step of the tiny result) and
+    the bits differ there; elsewhere, and for SiLU everywhere, at most 1 % of
+    the outputs differ in any bit.  M = 1 is the streaming GEMV, 5 and 12 the
+    MFMA GEMV (1 and 4 row tiles), 40 and 256 GEMM kernels."""
+    N, K = 256, 512
+    rng = np.random.default_rng(M * 10 + epi)
+    x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-13, -8, size=N)).astype(np.float32)
+    b = rng.integers(-8, 9, size=N).astype(np.float32) / np.float32(4)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), epi)
+    got_t = lin.forward(bf16_dev(x, dev))
+    got_bits, got = bf16_host_bits(got_t), bf16_host_f32(got_t)
+    ref_bits, ref = oracle.linear_w8a16(x, Q, s, b, epi)
+    ref = ref.astype(np.float64)
+    err = np.abs(got.astype(np.float64) - ref)
+    bound = np.maximum(np.abs(ref) * 2.0 ** -7, 1e-6)
+    worst = int(np.argmax(err - bound))
+    assert np.all(err <= bound), (worst, got.flat[worst], ref.flat[worst])
+    _, pre = oracle.linear_w8a16(x, Q, s, b, mj.EPI_NONE)  # exact pre-activation
+    keep = pre >= -2.0 if epi == mj.EPI_GELU_TANH else np.ones(pre.shape, bool)
+    frac = float(np.mean(got_bits[keep] != ref_bits[keep]))
+    print(f"M={M} epi={epi}: {frac:.4%} of {int(keep.sum())} outputs differ in some bit", flush=True)
+    assert frac <= 0.01
+    # the case spans the activation's range
+    assert float(pre.min()) < -4.0 and float(pre.max()) > 4.0 and np.mean(np.abs(pre) < 2) > 0.2
+
+
 def _mlp_case(oracle, M, K, I, H, seed):
     x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=seed))
     Wg, sg = oracle.quantize_rowwise_rhe(oracle.randn_f32((I, K), std=0.02, seed=seed + 6))
