@@ -43,6 +43,13 @@ extern "C" {
 #define MJ_EPI_SILU 3              /* silu32 (tensor/math.mojo:283-285)                      */
 #define MJ_EPI_GELU_TANH_APPROX 4  /* learn.nn gelu via _exp_approx (activations.mojo:158-163) */
 #define MJ_EPI_SILU_APPROX 5       /* learn.nn silu via _exp_approx (activations.mojo:137-152) */
+/* Entry points with fp32 outputs evaluate GELU_TANH and SILU literally (expf,
+ * IEEE division).  Entry points with bf16 outputs (the bf16 and W8A16 GEMMs,
+ * GEMVs and the FFN) evaluate the same functions as x / (1 + 2^(-2t log2 e))
+ * and x / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal: the bf16
+ * bits differ from the literal form's in a few outputs in 10^4 (near a
+ * rounding boundary) and, for GELU at x < -2, where the literal form's
+ * 1 + tanh cancels; every output stays within one bf16 step or 1e-6. */
 #define MJ_EPI_RELU_UNARY 6        /* Tensor.relu, apply_unary op 8 (tensor/math.mojo:582-585) */
 
 /* ---- int8 rounding rules -------------------------------------------- */
@@ -240,7 +247,7 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
 
 /* Llama-style FFN on W8A16 weights (composition of Linear, silu32 and the
  * elementwise product, tensor/tensor.mojo:4373):
- *   h[M,I] = bf16(silu32(x Wg^T * sg) * (x Wu^T * su))   (one fused GEMM)
+ *   h[M,I] = bf16(silu(x Wg^T * sg) * (x Wu^T * su))   (one fused GEMM; bf16-output silu)
  *   y[M,H] = bf16((h Wd^T) * sd)
  * Wg, Wu [I,K]; Wd [H,I]; h is a caller-owned [M,I] buffer. */
 int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
