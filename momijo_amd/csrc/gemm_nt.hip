@@ -197,13 +197,44 @@ __device__ __forceinline__ void stage_gateup(const GemmNT &p, const f32x4 (&acc)
   }
 }
 
-// Split-K: raw fp32 sums of this workgroup's K slice, 4 columns per store.
+// Split-K: raw fp32 sums of this workgroup's K slice.  A lane's block (i, j)
+// holds row 16i + (lane & 15), columns 16j + 4*(lane >> 4) + q: one 16-byte
+// store covers 64 bytes of 16 rows.  When the wave's whole sub-tile lies
+// inside C (N % 4 == 0), blocks j and j+1 are traded between lanes r and r+8
+// of each 16-lane row (DPP row_ror:8, bank-masked to the receiving half) so
+// that each store covers 128 contiguous bytes of 8 rows, whole lines.
 template <int TM, int TN, int WM, int WN>
 __device__ __forceinline__ void store_part8(const GemmNT &p, const f32x4 (&acc)[TM][TN], int m0,
                                             int n0, int wm, int wn, int lane, int split) {
   const int M = (int)p.M, N = (int)p.N;
   float *part = p.part + (size_t)split * M * N;
   const bool vec = (N & 3) == 0;
+  if constexpr (TN % 2 == 0) {
+    const int mw = m0 + wm * WM, nw = n0 + wn * WN;
+    if (vec && mw + TM * 16 <= M && nw + TN * 16 <= N) {
+      const int fr = lane & 15, fh = lane >> 4;
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        const int n = nw + (j + (fr >> 3)) * 16 + 4 * fh;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          float r0[4], r1[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int a = __float_as_int(acc[i][j][q]), b = __float_as_int(acc[i][j + 1][q]);
+            // rows 0-7 of the block: lanes 8-15 take block j+1 of lane - 8;
+            // rows 8-15: lanes 0-7 take block j of lane + 8
+            r0[q] = __int_as_float(__builtin_amdgcn_update_dpp(a, b, 0x128, 0xF, 0xC, false));
+            r1[q] = __int_as_float(__builtin_amdgcn_update_dpp(b, a, 0x128, 0xF, 0x3, false));
+          }
+          float *dst = part + (size_t)(mw + i * 16 + (fr & 7)) * N + n;
+          *(float4 *)dst = make_float4(r0[0], r0[1], r0[2], r0[3]);
+          *(float4 *)(dst + (size_t)8 * N) = make_float4(r1[0], r1[1], r1[2], r1[3]);
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int nb = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
