@@ -111,3 +111,34 @@ def test_bf16_matmul_through_tensor_surface(oracle, dev):
     W = mj.Tensor(bf16_dev(B, dev))
     C = x.matmul(W.transpose()).torch
     _check_rows(oracle, A, B, C, _rows(M))
+
+
+@pytest.mark.parametrize("M,N", [(4096, 4096), (300, 200)])
+@pytest.mark.parametrize("epi", [mj.EPI_GELU_TANH, mj.EPI_SILU])
+def test_bf16_gelu_silu_epilogue_exact_sums(oracle, dev, M, N, epi):
+    """bf16 GEMM epilogues evaluate GELU and SiLU in sigmoid form with the
+    hardware exp2 and reciprocal; with small-integer inputs (K = 16) the sums
+    are exact, so the activation alone separates them from the oracle's
+    literal expf/division forms: every output within one bf16 step (2^-7
+    relative) of the oracle's fp32 value or 1e-6 absolute, and at most 1 % of
+    the bits differing outside GELU's cancelling range x < -2.  4096 x 4096
+    runs the 256 x 256 one-wave-per-SIMD kernel (direct stores), 300 x 200
+    edge tiles through the staged epilogue."""
+    K = 16
+    rng = np.random.default_rng(M + N + epi)
+    A = oracle.f32_to_bf16(rng.integers(-2, 3, size=(M, K)).astype(np.float32))
+    B = oracle.f32_to_bf16(rng.integers(-1, 2, size=(N, K)).astype(np.float32))
+    bias = (rng.integers(-8, 9, size=N) / 4).astype(np.float32)
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev), to_dev(bias, dev), epi)
+    got_bits, got = bf16_host_bits(C), bf16_host_f32(C).astype(np.float64)
+    ref_bits, ref = oracle.gemm_bf16_nt(A, B, bias, epi)
+    _, pre = oracle.gemm_bf16_nt(A, B, bias, mj.EPI_NONE)
+    ref = ref.astype(np.float64)
+    err = np.abs(got - ref)
+    bound = np.maximum(np.abs(ref) * 2.0 ** -7, 1e-6)
+    assert np.all(err <= bound)
+    keep = pre >= -2.0 if epi == mj.EPI_GELU_TANH else np.ones(pre.shape, bool)
+    frac = float(np.mean(got_bits[keep] != ref_bits[keep]))
+    print(f"{M}x{N} epi={epi}: {frac:.4%} of {int(keep.sum())} outputs differ in some bit", flush=True)
+    assert frac <= 0.01
+    assert float(pre.min()) < -4.0 and float(pre.max()) > 4.0 and np.mean(np.abs(pre) < 2) > 0.2
