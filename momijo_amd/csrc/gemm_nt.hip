@@ -1305,7 +1305,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
 }
 
 static hipError_t launch_reduce(const GemmNT &p, hipStream_t stream) {
-  const int64_t total = p.M * ((p.N + 3) / 4);
+  // 8 columns per thread on the 16-byte path of the kernel, else 4
+  const bool vec8 = (p.N & 7) == 0 && (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0 &&
+                    p.splits <= 8;
+  const int64_t total = vec8 ? p.M * (p.N / 8) : p.M * ((p.N + 3) / 4);
   int64_t blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   const dim3 g((unsigned)blocks), b(256);
