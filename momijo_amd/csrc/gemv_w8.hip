@@ -1,6 +1,8 @@
 // Skinny-M W8A16 Linear (decode): y[m,n] = bf16(epi((x[m,:] . Q[n,:]) *
 // scales[n] + bias[n])) for M <= 16, int8 weights Q [N,K] streamed once:
-// the streaming kernel below for M <= 2, the MFMA kernel after it above.
+// the persistent streaming kernel (gemv_w8a16_stream_kernel, further down) for
+// M = 1 and K <= 4096, the streaming kernel below for the other M <= 2, the
+// MFMA kernel after it above.
 //
 // The streaming kernel is HBM-bound (1 byte of weight per multiply-add), so the design
 // goal is bytes in flight: each wave owns RPW consecutive weight rows and
@@ -37,7 +39,9 @@ __global__ __launch_bounds__(256) void gemv_w8a16_kernel(const uint16_t *__restr
                                                          int K) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[XLDS ? kGemvXsElems : 8];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // uniform wave index: the buffer resource below is then known to be
+  // wave-uniform (a divergent one costs a readfirstlane loop per load)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = (blockIdx.x * 4 + wave) * RPW;
   const int nchunks = K >> 4;  // 16-element chunks per row
   const int rows = N - row0 < RPW ? N - row0 : RPW;  // <= 0 for trailing waves
@@ -271,6 +275,186 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
   }
 }
 
+// Decode GEMV for one x row (M = 1, K = 1024, 2048, 3072 or 4096): persistent
+// streaming.
+//
+// One workgroup per CU (the grid stays below the CU count: a second workgroup
+// on a CU doubles that CU's share of the weight stream, and 256 workgroups on
+// the 256-CU part measured as slow as 276).  A workgroup owns 4*RW
+// consecutive weight rows; wave v takes rows v, v + 4, v + 8, ... so the four
+// waves of a CU read neighbouring 4-KB rows at each step.  x is loaded first,
+// straight into registers, and converted to fp32 once per wave: lane l owns k
+// chunks l, l + 64, ... of 16 elements, for every row.  Each row is four 1-KB
+// nontemporal loads (16 bytes per lane); D rows are in flight per wave and the
+// loads of row r + D are issued after row r's arithmetic (sched_barrier fences
+// keep that order: left free, the scheduler grouped the issues of several rows
+// and the stream stalled).  The row dot is 64 widening multiply-adds per lane;
+// four rows' lane sums are reduced together (two v_permlane32_swap, one
+// v_permlane16_swap and four DPP adds leave row j's total in 16-lane row j),
+// then scale, bias and the activation are applied and 16-lane row j stores
+// its output.  The row index arithmetic uses a wave index taken through
+// readfirstlane: otherwise the compiler treats the per-wave buffer resource as
+// divergent and wraps every load in a readfirstlane loop.
+//
+// Measured on MI355X, 11008 x 4096 (graph replay over 8 weight copies that do
+// not fit the MALL, interleaved A/B in one process): 8.43 us against 9.79 us
+// for the 2-rows-per-wave kernel above; a pure 45 MB read takes 7.72 us.
+constexpr int kGemvStreamMaxWgs = 252;
+
+__device__ __forceinline__ float dpp_row_sum(float v) {
+#define MJ_DPP_F(v, ctrl) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false))
+  v += MJ_DPP_F(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += MJ_DPP_F(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += MJ_DPP_F(v, 0x124);  // row_ror:4
+  v += MJ_DPP_F(v, 0x128);  // row_ror:8
+#undef MJ_DPP_F
+  return v;
+}
+
+// Lane partial sums p0..p3 of four rows -> every lane of 16-lane row j holds
+// the 64-lane total of p_j.
+__device__ __forceinline__ float reduce4_rows(float p0, float p1, float p2, float p3) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(p0), __float_as_uint(p2), false,
+                                                  false);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(p1), __float_as_uint(p3), false,
+                                                  false);
+  // lanes 0-31: p0 (p1) halves summed, lanes 32-63: p2 (p3)
+  const float r02 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const float r13 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13),
+                                                  false, false);
+  return dpp_row_sum(__uint_as_float(c[0]) + __uint_as_float(c[1]));
+}
+
+template <int CPL, int RW, int D>
+__global__ __launch_bounds__(256) void gemv_w8a16_stream_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const float *__restrict__ scales,
+    const float *__restrict__ bias, int epi, uint16_t *__restrict__ y, int N, int K) {
+  constexpr int NG = (RW + 3) / 4;  // groups of four rows reduced together
+  constexpr int NS = D;             // weight register slots
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 4 * RW + wave;  // rows row0 + 4 i
+  if (row0 >= N) return;
+  const int rows = (N - row0 + 3) / 4 < RW ? (N - row0 + 3) / 4 : RW;
+
+  // lane 16 j + g (g < NG) finishes the wave's row 4 g + j, i.e. weight row
+  // row0 + 4 (4 g + j): its scale and bias are loaded first
+  const int my_rr = 4 * (lane & 15) + (lane >> 4);
+  const bool my_out = (lane & 15) < NG && my_rr < rows;
+  const int my_n = row0 + 4 * (my_rr < rows ? my_rr : rows - 1);
+  const float my_s = scales[my_n];
+  const float my_b = bias ? bias[my_n] : 0.0f;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)K * 2);
+  uint4 xa[CPL], xb[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)((c * 64 + lane) * 32), 0, 0);
+    const u32x4 b =
+        __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)((c * 64 + lane) * 32 + 16), 0, 0);
+    xa[c] = make_uint4(a[0], a[1], a[2], a[3]);
+    xb[c] = make_uint4(b[0], b[1], b[2], b[3]);
+  }
+  const __amdgpu_buffer_rsrc_t rQ =
+      make_rsrc(Q + (size_t)row0 * K, (int64_t)(4 * (rows - 1) + 1) * K);
+  uint4 q[NS][CPL];
+  // K == 1024 * CPL: every lane chunk lies inside the row, so the only
+  // per-load choice is a select on the row (rows past the wave's read zero);
+  // a per-chunk test compiled into branches around every load
+  auto issue = [&](int r, int slot) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t off = r < rows ? (uint32_t)(4 * r * K + (c * 64 + lane) * 16) : kOobOffset;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rQ, off, 0, 2 /* nt */);
+      q[slot][c] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(d, d);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float xf[CPL][16];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const uint32_t xw[8] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w, xb[c].x, xb[c].y, xb[c].z, xb[c].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xf[c][2 * e] = __uint_as_float(xw[e] << 16);
+      xf[c][2 * e + 1] = __uint_as_float(xw[e] & 0xFFFF0000u);
+    }
+  }
+
+  float part[4], tot[NG];
+#pragma unroll
+  for (int r = 0; r < NG * 4; ++r) {
+    float a = 0.0f;
+    if (r < RW) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t qw[4] = {q[r % NS][c].x, q[r % NS][c].y, q[r % NS][c].z, q[r % NS][c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t v = (int32_t)qw[e];
+          a += xf[c][4 * e + 0] * (float)((v << 24) >> 24);
+          a += xf[c][4 * e + 1] * (float)((v << 16) >> 24);
+          a += xf[c][4 * e + 2] * (float)((v << 8) >> 24);
+          a += xf[c][4 * e + 3] * (float)(v >> 24);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (r + D < RW) issue(r + D, r % NS);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    part[r % 4] = a;
+    if (r % 4 == 3) tot[r / 4] = reduce4_rows(part[0], part[1], part[2], part[3]);
+  }
+  // every lane of 16-lane row j holds tot[g] = row 4 g + j: lane 16 j + g
+  // takes tot[g], so one activation evaluation covers all groups (an
+  // epilogue per group, with the activation switch, made the kernel 1 us
+  // slower: 2370 instructions against ~1900)
+  float t = tot[0];
+#pragma unroll
+  for (int g = 1; g < NG; ++g) t = (lane & 15) == g ? tot[g] : t;
+  float v;
+  {
+#pragma clang fp contract(off)
+    v = t * my_s;
+    if (bias) v = v + my_b;
+  }
+  v = apply_epi_b16(epi, v);
+  if (my_out) y[my_n] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+template <int CPL, int RW>
+static void launch_stream(const uint16_t *x, const int8_t *Q, const float *scales,
+                          const float *bias, int epi, uint16_t *y, int64_t N, int64_t K,
+                          hipStream_t stream) {
+  constexpr int D = RW < 3 ? RW : 3;
+  const unsigned grid = (unsigned)((N + 4 * RW - 1) / (4 * RW));
+  hipLaunchKernelGGL((gemv_w8a16_stream_kernel<CPL, RW, D>), dim3(grid), dim3(256), 0, stream, x,
+                     Q, scales, bias, epi, y, (int)N, (int)K);
+}
+
+template <int CPL>
+static void launch_stream_rw(const uint16_t *x, const int8_t *Q, const float *scales,
+                             const float *bias, int epi, uint16_t *y, int64_t N, int64_t K,
+                             hipStream_t stream) {
+  // fewest rows per wave that keep the grid within kGemvStreamMaxWgs
+  // workgroups (larger N: 32 rows per wave and more workgroups)
+  const int64_t need = (N + 4 * kGemvStreamMaxWgs - 1) / (4 * kGemvStreamMaxWgs);
+  if (need <= 1) return launch_stream<CPL, 1>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 2) return launch_stream<CPL, 2>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 4) return launch_stream<CPL, 4>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 6) return launch_stream<CPL, 6>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 8) return launch_stream<CPL, 8>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 11) return launch_stream<CPL, 11>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 16) return launch_stream<CPL, 16>(x, Q, scales, bias, epi, y, N, K, stream);
+  if (need <= 24) return launch_stream<CPL, 24>(x, Q, scales, bias, epi, y, N, K, stream);
+  return launch_stream<CPL, 32>(x, Q, scales, bias, epi, y, N, K, stream);
+}
+
 template <int MB>
 static hipError_t launch_mb(const uint16_t *x, const int8_t *Q, const float *scales,
                             const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
@@ -312,6 +496,14 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
       hipLaunchKernelGGL((gemv_w8a16_mfma_kernel<4, 1>), dim3((unsigned)((N + 15) / 16)),
                          dim3(256), 0, stream, x, Q, scales, bias, epi, y, (int)M, (int)N,
                          (int)K);
+    return hipGetLastError();
+  }
+  if (M == 1 && K % 1024 == 0 && K <= 4096 && K > 0) {
+    // (a wave's rows span 4 (RW - 1) + 1 <= 125 rows of K bytes: 32-bit offsets)
+    if (K == 1024) launch_stream_rw<1>(x, Q, scales, bias, epi, y, N, K, stream);
+    else if (K == 2048) launch_stream_rw<2>(x, Q, scales, bias, epi, y, N, K, stream);
+    else if (K == 3072) launch_stream_rw<3>(x, Q, scales, bias, epi, y, N, K, stream);
+    else launch_stream_rw<4>(x, Q, scales, bias, epi, y, N, K, stream);
     return hipGetLastError();
   }
   if (M <= 1) return launch_mb<1>(x, Q, scales, bias, epi, y, M, N, K, stream);

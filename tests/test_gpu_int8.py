@@ -236,7 +236,16 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    # skinny-M MFMA GEMV: partial 16-row tile of
                                    # weights, K % 64 != 0, x rows < 16
                                    (3, 4104, 1040), (16, 1000, 4096),
-                                   (7, 37, 80)])
+                                   (7, 37, 80),
+                                   # M = 1: the persistent streaming GEMV (K a
+                                   # multiple of 1024) at every rows-per-wave
+                                   # (1..32) and K-chunk count (1..4), with
+                                   # partial last workgroups and waves; other K
+                                   # take the 2-rows-per-wave kernel
+                                   (1, 37, 1024), (1, 1500, 2048), (1, 4104, 3072),
+                                   (1, 5000, 4096), (1, 7001, 3072), (1, 11008, 4096),
+                                   (1, 16001, 1024), (1, 24000, 2048), (1, 70001, 1024),
+                                   (1, 37, 80), (1, 4104, 2064)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
