@@ -47,6 +47,13 @@ hipStream_t S(void *stream) { return (hipStream_t)stream; }
 // Plans and launches an NT GEMM, with a stream-ordered fp32 workspace when the
 // plan splits K.
 int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
+  // The tile kernels address a tile's 256 rows of A and of B with 32-bit
+  // buffer offsets ((r * ld + k) * element size, r < 256): larger leading
+  // dimensions would wrap or fall outside the buffer resource and read zeros.
+  const int64_t bsz = p.bkind == mj::B_INT8 ? 1 : 2;
+  if (256 * p.lda * 2 >= ((int64_t)1 << 31) || 256 * p.ldb * bsz >= ((int64_t)1 << 31))
+    return fail(MJ_ERR_UNSUPPORTED, "%s: leading dimension too large for 32-bit tile offsets "
+                "(lda=%lld, ldb=%lld)", what, (long long)p.lda, (long long)p.ldb);
   const mj::GemmPlan plan = mj::plan_gemm_nt(p);
   const size_t ws = plan.workspace_bytes(p);
   if (ws) {

@@ -27,12 +27,23 @@ __device__ __forceinline__ int quant_legacy(float x, float scale) {
   return (int)t;
 }
 
-// round half to even, clamp to [-127, 127].
+// round half to even, clamp to [-127, 127]; NaN -> 0 (a NaN weight, or a
+// NaN scale, quantizes to zero instead of an undefined float-to-int cast).
 __device__ __forceinline__ int quant_rhe(float x, float scale) {
   float v = __builtin_rintf(x / scale);
+  if (v != v) return 0;
   v = v > 127.0f ? 127.0f : v;
   v = v < -127.0f ? -127.0f : v;
   return (int)v;
+}
+
+// MinMaxObserver.observe's NaN rule (sequential.mojo:232-240): min and max
+// start at the first element and are replaced only when v < mn / v > mx, so
+// a NaN first element makes both NaN and later NaNs are skipped.  The
+// reductions use fminf / fmaxf, which skip every NaN; this restores the first
+// element's case.
+__device__ __forceinline__ void observer_nan_rule(float first, float &mn, float &mx) {
+  if (first != first) mn = mx = first;
 }
 
 __device__ __forceinline__ float row_scale(int rounding, float amax, float mn, float mx) {
@@ -83,6 +94,7 @@ __global__ __launch_bounds__(256) void quantize_rowwise_reg(const float *__restr
   amax = wave_max(amax);
   mn = wave_min(mn);
   mx = wave_max(mx);
+  observer_nan_rule(__shfl(w[0].x, 0, 64), mn, mx);
   const float s = row_scale(rounding, amax, mn, mx);
   uint32_t *q4 = (uint32_t *)(Q + (size_t)row * K);
 #pragma unroll
@@ -109,6 +121,7 @@ __global__ __launch_bounds__(256) void quantize_rowwise_any(const float *__restr
   amax = wave_max(amax);
   mn = wave_min(mn);
   mx = wave_max(mx);
+  observer_nan_rule(w[0], mn, mx);
   const float s = row_scale(rounding, amax, mn, mx);
   for (int k = lane; k < K; k += 64)
     Q[(size_t)row * K + k] = (int8_t)(rounding == ROUND_RHE ? quant_rhe(w[k], s) : quant_legacy(w[k], s));
@@ -185,7 +198,8 @@ __global__ __launch_bounds__(256) void minmax_partial_kernel(const float *__rest
 
 // Folds the partials; with max_q < 0 it writes {min, max} instead of the
 // scale.
-__global__ __launch_bounds__(64) void minmax_final_kernel(const float *__restrict__ part, int np,
+__global__ __launch_bounds__(64) void minmax_final_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ part, int np,
                                                           int64_t n, float max_q,
                                                           float *__restrict__ out) {
   float mn = __builtin_inff(), mx = -__builtin_inff();
@@ -195,6 +209,7 @@ __global__ __launch_bounds__(64) void minmax_final_kernel(const float *__restric
   }
   mn = wave_min(mn);
   mx = wave_max(mx);
+  if (n > 0) observer_nan_rule(x[0], mn, mx);
   if (threadIdx.x == 0 && max_q < 0.0f) {
     out[0] = mn;
     out[1] = mx;
@@ -219,8 +234,8 @@ static hipError_t minmax_impl(const float *x, int64_t n, float max_q, float *par
                      partials);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(minmax_final_kernel, dim3(1), dim3(64), 0, stream, partials, (int)blocks, n,
-                     max_q, out);
+  hipLaunchKernelGGL(minmax_final_kernel, dim3(1), dim3(64), 0, stream, x, partials, (int)blocks,
+                     n, max_q, out);
   return hipGetLastError();
 }
 

@@ -107,14 +107,33 @@ class QuantLinear:
                  s_w: float, s_x: float, legacy_literal: bool = False):
         self.in_features = in_features
         self.out_features = out_features
-        self.w_q = Tensor(w_q.torch.contiguous())
-        self.b_f = Tensor(b_f.torch.contiguous())
+        wq, bf = w_q.torch, b_f.torch
+        # the kernels read w_q [out, in] and b_f [out] in full: wrong shapes
+        # would read past the allocations (the reference indexes them
+        # unchecked, layers.mojo:1681-1685, functional.mojo:281-302)
+        if wq.dtype != torch.int8 or tuple(wq.shape) != (out_features, in_features):
+            raise ValueError(f"w_q must be int8 [{out_features}, {in_features}], "
+                             f"got {wq.dtype} {list(wq.shape)}")
+        if bf.dtype != torch.float32 or bf.numel() != out_features:
+            raise ValueError(f"b_f must be float32 with {out_features} elements, "
+                             f"got {bf.dtype} with {bf.numel()}")
+        self.w_q = Tensor(wq.contiguous())
+        self.b_f = Tensor(bf.reshape(-1).contiguous())
         self.s_w = float(np.float32(s_w))
         self.s_x = float(np.float32(s_x))
         self.legacy_literal = legacy_literal
 
     def forward(self, x: Tensor) -> Tensor:
-        xt = x.torch.contiguous()
+        """A non-2-D x or a width other than in_features gives the reference's
+        empty [0, 0] result (matmul_i8_i8_to_i32 returns [0, 0] and
+        dequantize_i32_to_f32_add_bias keeps it, functional.mojo:253-263,
+        291-292)."""
+        xt = x.torch
+        if xt.dim() != 2 or xt.shape[1] != self.in_features:
+            return Tensor(torch.zeros((0, 0), dtype=torch.float32, device=_device()))
+        if xt.dtype != torch.float32:
+            raise TypeError("QuantLinear takes Float32 inputs")
+        xt = xt.contiguous()
         M, K = xt.shape
         N = self.out_features
         y = torch.empty((M, N), dtype=torch.float32, device=xt.device)
@@ -135,11 +154,17 @@ class W8Linear:
 
     def __init__(self, q: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None,
                  epi: int = _lib.EPI_NONE):
+        if q.dtype != torch.int8 or q.dim() != 2:
+            raise ValueError(f"q must be a 2-D int8 tensor, got {q.dtype} {list(q.shape)}")
         self.q = q.contiguous()
-        self.scales = scales.contiguous()
-        self.bias = None if bias is None else bias.float().contiguous()
-        self.epi = epi
         self.out_features, self.in_features = self.q.shape
+        if scales.dtype != torch.float32 or scales.numel() != self.out_features:
+            raise ValueError(f"scales must be float32 with {self.out_features} elements")
+        if bias is not None and bias.numel() != self.out_features:
+            raise ValueError(f"bias must have {self.out_features} elements")
+        self.scales = scales.reshape(-1).contiguous()
+        self.bias = None if bias is None else bias.float().reshape(-1).contiguous()
+        self.epi = epi
 
     @classmethod
     def from_float(cls, W: torch.Tensor, bias: torch.Tensor | None = None,
@@ -148,11 +173,10 @@ class W8Linear:
         return cls(q, s, bias, epi)
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        M, K = x.shape
-        if K != self.in_features:
-            raise ValueError(f"expected {self.in_features} input features, got {K}")
+        M, K = _check_bf16_rows(x, self.in_features, "x")
         if out is None:
             out = torch.empty((M, self.out_features), dtype=torch.bfloat16, device=x.device)
+        _check_bf16_out(out, (M, self.out_features), "out")
         _lib.call("mj_linear_w8a16", _ptr(x), _ptr(self.q), _ptr(self.scales), _ptr(self.bias),
                   self.epi, _ptr(out), M, self.out_features, K, _stream())
         return out
@@ -169,17 +193,37 @@ class W8MLP:
 
     def forward(self, x: torch.Tensor, h: torch.Tensor | None = None,
                 out: torch.Tensor | None = None):
-        M, K = x.shape
+        M, K = _check_bf16_rows(x, self.gate.in_features, "x")
         I = self.gate.out_features
         H = self.down.out_features
         if h is None:
             h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
         if out is None:
             out = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+        _check_bf16_out(h, (M, I), "h")
+        _check_bf16_out(out, (M, H), "out")
         _lib.call("mj_mlp_w8a16", _ptr(x), _ptr(self.gate.q), _ptr(self.gate.scales),
                   _ptr(self.up.q), _ptr(self.up.scales), _ptr(self.down.q),
                   _ptr(self.down.scales), _ptr(h), _ptr(out), M, K, I, H, _stream())
         return out, h
+
+
+def _check_bf16_rows(x: torch.Tensor, K: int, name: str) -> tuple[int, int]:
+    """x must be a contiguous bfloat16 [M, K] device tensor: the C ABI takes
+    its leading dimension as K."""
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {x.dtype}")
+    if x.dim() != 2 or x.shape[1] != K:
+        raise ValueError(f"{name} must be [M, {K}], got {list(x.shape)}")
+    if not x.is_contiguous():
+        raise ValueError(f"{name} must be contiguous (row stride == {K})")
+    return int(x.shape[0]), K
+
+
+def _check_bf16_out(t: torch.Tensor, shape: tuple, name: str) -> None:
+    if t.dtype != torch.bfloat16 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous bfloat16 {list(shape)} tensor, got "
+                         f"{t.dtype} {list(t.shape)}")
 
 
 def quantize_rowwise_int8(W: torch.Tensor, rounding: int = _lib.ROUND_RHE):

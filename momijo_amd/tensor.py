@@ -291,11 +291,24 @@ def tensordot(A: Tensor, B: Tensor, axes: int = 1) -> Tensor:
 
 def gemm_bf16_nt(A: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None,
                  epi: int = _lib.EPI_NONE, out: torch.Tensor | None = None) -> torch.Tensor:
-    """C = bf16(epi(A @ W^T + bias)) for bf16 device tensors A [M,K], W [N,K]."""
+    """C = bf16(epi(A @ W^T + bias)) for bf16 device tensors A [M,K], W [N,K]
+    with unit column stride (row strides are passed as leading dimensions)."""
+    if A.dtype != torch.bfloat16 or W.dtype != torch.bfloat16:
+        raise TypeError(f"gemm_bf16_nt takes bfloat16 A and W, got {A.dtype} and {W.dtype}")
+    if A.dim() != 2 or W.dim() != 2 or A.shape[1] != W.shape[1]:
+        raise ValueError(f"gemm_bf16_nt: A [M,K] and W [N,K] expected, got {list(A.shape)} "
+                         f"and {list(W.shape)}")
+    if A.stride(1) != 1 or W.stride(1) != 1:
+        raise ValueError("gemm_bf16_nt: A and W need unit column stride")
     M, K = A.shape
     N = W.shape[0]
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N):
+        raise ValueError(f"gemm_bf16_nt: bias must be float32 with {N} elements")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"gemm_bf16_nt: out must be bfloat16 [{M}, {N}] with unit column "
+                         "stride")
     _lib.call("mj_gemm_bf16_nt", M, N, K, _ptr(A), A.stride(0), _ptr(W), W.stride(0), _ptr(bias),
               epi, _ptr(out), out.stride(0), _stream())
     return out

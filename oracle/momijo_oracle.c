@@ -459,7 +459,8 @@ MO_API void mo_quant_linear_fw(const float *x, const int8_t *Wq, const float *b,
 /* ------------------------------------------------------------------------ */
 
 /* scale[n] = max_k |W[n,k]| / 127 (fp32 division); q = clamp(rne(W/scale),
- * -127, 127).  rintf rounds half to even in the default FP environment. */
+ * -127, 127).  rintf rounds half to even in the default FP environment.
+ * NaN weights do not enter the absmax (a > m is false) and quantize to 0. */
 MO_API void mo_quantize_rowwise_rhe(const float *W, int64_t N, int64_t K, int8_t *Q, float *scales) {
     for (int64_t n = 0; n < N; ++n) {
         const float *w = W + n * K;
@@ -473,6 +474,7 @@ MO_API void mo_quantize_rowwise_rhe(const float *W, int64_t N, int64_t K, int8_t
         scales[n] = s;
         for (int64_t k = 0; k < K; ++k) {
             float v = rintf(w[k] / s);
+            if (v != v) v = 0.0f;
             if (v > 127.0f) v = 127.0f;
             if (v < -127.0f) v = -127.0f;
             Q[n * K + k] = (int8_t)v;

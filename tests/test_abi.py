@@ -83,6 +83,21 @@ def test_validation_status_codes(lib):
     assert lib.mj_matmul_i8_i8_to_i32(p, p, p, big, 1, 1, 0, None) == _lib.MJ_ERR_UNSUPPORTED
 
 
+def test_tile_offset_range_guard(lib):
+    """The GEMM tiles address 256 rows with 32-bit byte offsets: a leading
+    dimension with 256 * ld * element size >= 2^31 is refused before any
+    device work (otherwise loads would wrap or read zeros)."""
+    p = ctypes.c_void_p(4096)  # 16-byte aligned, never dereferenced
+    ld = 1 << 22               # 256 * 2^22 * 2 bytes = 2^31
+    for lda, ldb in ((ld, 16), (16, ld)):
+        st = lib.mj_gemm_bf16_nt(300, 300, 16, p, lda, p, ldb, None, 0, p, 300, None)
+        assert st == _lib.MJ_ERR_UNSUPPORTED, (lda, ldb, _err(lib))
+        assert "32-bit tile offsets" in _err(lib)
+    # int8 weights are 1 byte per element: ld = 2^22 fits, 2^23 does not (x
+    # is bf16 with lda = K, so K = 2^22 is refused on the activation side)
+    assert lib.mj_linear_w8a16(p, p, p, None, 0, p, 300, 8, 1 << 22, None) == _lib.MJ_ERR_UNSUPPORTED
+
+
 def test_empty_problems_are_noops(lib):
     p = ctypes.c_void_p(16)
     assert lib.mj_matmul_f32(0, 5, 3, None, 3, 1, None, 5, 1, None, 0, p, 5, None) == _lib.MJ_OK

@@ -173,3 +173,66 @@ def test_w8a16_output_rounding_special_values(oracle, dev, M):
     assert bad[0].size == 0, (f"{bad[0].size} mismatches, first at {bad[0][0]},{bad[1][0]}: "
                               f"in {bias.view(np.uint32)[bad[1][0]]:#010x} "
                               f"got {got[bad[0][0], bad[1][0]]:#06x} want {want[bad[1][0]]:#06x}")
+
+
+# ------------------------------------------------------------- host-side validation
+def test_quant_linear_shape_mismatch_returns_empty(oracle, dev):
+    """QuantLinear.forward on a non-2-D x or a width other than in_features
+    returns the reference's empty [0, 0] result (matmul_i8_i8_to_i32's
+    fallback, functional.mojo:253-263) instead of reading past w_q."""
+    Wq = np.zeros((8, 16), np.int8)
+    q = mj.QuantLinear(16, 8, mj.Tensor(to_dev(Wq, dev)),
+                       mj.Tensor(to_dev(np.zeros(8, np.float32), dev)), 0.1, 0.1)
+    for shape in ((4, 32), (4, 8), (16,), (2, 4, 16)):
+        y = q.forward(mj.Tensor(to_dev(np.ones(shape, np.float32), dev)))
+        assert y.shape() == [0, 0] and y.dtype == torch.float32
+    assert q.forward(mj.Tensor(to_dev(np.ones((3, 16), np.float32), dev))).shape() == [3, 8]
+    with pytest.raises(ValueError):   # w_q not [out, in]
+        mj.QuantLinear(16, 8, mj.Tensor(to_dev(np.zeros((16, 8), np.int8), dev)),
+                       mj.Tensor(to_dev(np.zeros(8, np.float32), dev)), 0.1, 0.1)
+    with pytest.raises(ValueError):   # bias length
+        mj.QuantLinear(16, 8, mj.Tensor(to_dev(Wq, dev)),
+                       mj.Tensor(to_dev(np.zeros(7, np.float32), dev)), 0.1, 0.1)
+
+
+def test_w8_layers_reject_bad_operands(dev):
+    q = torch.zeros((32, 64), dtype=torch.int8, device=dev)
+    s = torch.ones(32, dtype=torch.float32, device=dev)
+    lin = mj.W8Linear(q, s)
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
+    assert lin.forward(x).shape == (4, 32)
+    with pytest.raises(TypeError):
+        lin.forward(x.float())
+    with pytest.raises(ValueError):
+        lin.forward(torch.zeros((4, 128), dtype=torch.bfloat16, device=dev))
+    with pytest.raises(ValueError):   # row-strided view: the ABI takes lda = K
+        lin.forward(torch.zeros((4, 128), dtype=torch.bfloat16, device=dev)[:, :64])
+    with pytest.raises(ValueError):
+        lin.forward(x, out=torch.empty((4, 31), dtype=torch.bfloat16, device=dev))
+    with pytest.raises(ValueError):
+        mj.W8Linear(q, s[:31])
+    down = mj.W8Linear(torch.zeros((64, 32), dtype=torch.int8, device=dev),
+                       torch.ones(64, dtype=torch.float32, device=dev))
+    mlp = mj.W8MLP(lin, mj.W8Linear(q, s), down)
+    y, h = mlp.forward(x)
+    assert y.shape == (4, 64) and h.shape == (4, 32)
+    with pytest.raises(ValueError):   # x wider than the gate's in_features
+        mlp.forward(torch.zeros((4, 96), dtype=torch.bfloat16, device=dev))
+    with pytest.raises(ValueError):
+        mlp.forward(x, h=torch.empty((4, 16), dtype=torch.bfloat16, device=dev))
+    with pytest.raises(TypeError):
+        mlp.forward(x.float())
+
+
+def test_gemm_bf16_nt_rejects_bad_operands(dev):
+    A = torch.zeros((8, 32), dtype=torch.bfloat16, device=dev)
+    W = torch.zeros((16, 32), dtype=torch.bfloat16, device=dev)
+    assert mj.gemm_bf16_nt(A, W).shape == (8, 16)
+    with pytest.raises(TypeError):
+        mj.gemm_bf16_nt(A.float(), W)
+    with pytest.raises(ValueError):   # K mismatch
+        mj.gemm_bf16_nt(A, torch.zeros((16, 48), dtype=torch.bfloat16, device=dev))
+    with pytest.raises(ValueError):   # transposed operand (column stride != 1)
+        mj.gemm_bf16_nt(A, torch.zeros((32, 16), dtype=torch.bfloat16, device=dev).t())
+    with pytest.raises(ValueError):
+        mj.gemm_bf16_nt(A, W, out=torch.empty((8, 8), dtype=torch.bfloat16, device=dev))

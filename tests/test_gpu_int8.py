@@ -88,6 +88,33 @@ def test_minmax_scale(oracle, dev):
     assert zero == 1.0
 
 
+def test_minmax_and_quantize_nan(oracle, dev):
+    """NaN semantics against the oracle: the observer's first-element rule
+    (sequential.mojo:232-240) for mj_minmax_* and the legacy per-row scale,
+    NaN -> 0 for both quantizers."""
+    nan = np.float32(np.nan)
+    x = oracle.randn_f32((3000,), seed=11)
+    x[[7, 1500, 2999]] = nan
+    got = mj.functional.scale_symmetric_device(mj.Tensor(to_dev(x, dev)))
+    assert np.float32(got) == np.float32(oracle.minmax_scale_symmetric(x))
+    x[0] = nan
+    assert np.isnan(mj.functional.scale_symmetric_device(mj.Tensor(to_dev(x, dev))))
+    obs = mj.MinMaxObserver()
+    obs.observe(mj.Tensor(to_dev(x, dev)))
+    assert np.isnan(obs.min_v) and np.isnan(obs.max_v) and np.isnan(obs.scale_symmetric())
+    W = oracle.randn_f32((6, 4096), std=0.02, seed=12)   # register path (K % 256 == 0)
+    W[0, 0] = W[1, 100] = W[2, :] = nan
+    W2 = oracle.randn_f32((3, 100), std=0.02, seed=13)   # generic path
+    W2[0, 0] = W2[1, 7] = nan
+    for w in (W, W2):
+        for rounding in (mj.ROUND_RHE, mj.ROUND_LEGACY):
+            q, sc = _quant_dev(w, dev, rounding)
+            ref = oracle.quantize_rowwise_rhe(w) if rounding == mj.ROUND_RHE else \
+                oracle.quantize_rowwise_legacy(w)
+            np.testing.assert_array_equal(q.cpu().numpy(), ref[0])
+            np.testing.assert_array_equal(sc.cpu().numpy(), ref[1])   # NaN == NaN here
+
+
 # ------------------------------------------------------------- int8 GEMM (legacy)
 @pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (64, 64, 64), (37, 53, 80), (5, 7, 10), (200, 300, 1024),
                                    (130, 129, 16)])

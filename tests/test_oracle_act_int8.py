@@ -128,6 +128,30 @@ def test_minmax_scale_rules(oracle):
     assert oracle.minmax_scale_symmetric(-x) == f32(3.5) / f32(127)
 
 
+def test_minmax_nan_rule(oracle):
+    """observe() starts min/max at x[0] and replaces them only on v < mn /
+    v > mx (sequential.mojo:232-240): under IEEE comparisons a NaN first
+    element stays (both bounds NaN, so scale_symmetric returns NaN / max_q,
+    its m <= 0 guard being false for NaN), and any later NaN is skipped."""
+    nan = np.float32(np.nan)
+    assert np.isnan(oracle.minmax_scale_symmetric(np.array([nan, 1.0, -2.0], np.float32)))
+    assert oracle.minmax_scale_symmetric(np.array([1.0, nan, -2.0], np.float32)) == f32(2) / f32(127)
+    assert oracle.minmax_scale_symmetric(np.array([0.5, -0.25, nan], np.float32)) == f32(0.5) / f32(127)
+
+
+def test_rhe_quantize_nan(oracle):
+    """Per-channel RHE: a NaN weight quantizes to 0 and does not enter the
+    row's absmax (a > m is false for NaN); an all-NaN row keeps scale 1."""
+    nan = np.float32(np.nan)
+    W = np.array([[nan, 0.5, -1.0, 0.25], [nan, nan, nan, nan]], np.float32)
+    Q, s = oracle.quantize_rowwise_rhe(W)
+    assert s[0] == f32(1.0) / f32(127) and s[1] == 1.0
+    np.testing.assert_array_equal(Q, np.array([[0, 64, -127, 32], [0, 0, 0, 0]], np.int8))
+    Ql, sl = oracle.quantize_rowwise_legacy(W)
+    assert np.isnan(sl[0]) and np.isnan(sl[1])   # NaN first element: the observer's NaN scale
+    assert not Ql.any()                           # and every q from a NaN quotient is 0
+
+
 def test_quant_linear_composition(oracle):
     x = oracle.randn_f32((6, 32), seed=4)
     W = oracle.randn_f32((8, 32), std=0.1, seed=5)
