@@ -4,8 +4,8 @@
  * bias + activation epilogue.
  *
  * Every entry point is `extern "C"`, takes plain pointers and sizes, returns
- * an int32 status (MJ_OK = 0) and never throws.  Unless a name ends in `_h`,
- * pointers are DEVICE pointers (HIP global memory of the current device) and
+ * an int32 status (MJ_OK = 0) and never throws.  Unless a name ends in `_h`
+ * (or is one of the memory-copy entry points), pointers are DEVICE pointers (HIP global memory of the current device) and
  * the call is asynchronous on `stream` (a hipStream_t; NULL = the null
  * stream).  `_h` variants take HOST pointers, copy in, run and copy out
  * synchronously, which is the ownership model of the reference's own device
@@ -254,6 +254,117 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
                      const int8_t *Wu, const float *su, const int8_t *Wd, const float *sd,
                      uint16_t *h, uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H,
                      void *stream);
+
+/* ---- device memory and streams (api_host.hip) -------------------------- */
+/* For a caller that keeps tensors resident across calls (e.g. QuantLinear's
+ * w_q uploaded once).  momijo itself has no device-resident tensors
+ * (tensor/device.mojo:258-302: to_device round-trips through the host); the
+ * reference seam allocates per call with DeviceContext.enqueue_create_buffer
+ * (tensor/gpu/runtime.mojo:563-570), which these replace. */
+
+/* *ptr = device allocation of `bytes` bytes (NULL for 0). */
+int32_t mj_malloc(void **ptr, int64_t bytes);
+/* Frees an mj_malloc allocation (NULL is a no-op). */
+int32_t mj_free(void *ptr);
+/* Synchronous copies: ordered after the work queued on `stream` (NULL = the
+ * null stream) and complete when they return, like the reference's
+ * enqueue_copy + synchronize (runtime.mojo:586-598). */
+int32_t mj_memcpy_htod(void *dst_device, const void *src_host, int64_t bytes, void *stream);
+int32_t mj_memcpy_dtoh(void *dst_host, const void *src_device, int64_t bytes, void *stream);
+/* Asynchronous device-to-device copy on `stream`. */
+int32_t mj_memcpy_dtod(void *dst_device, const void *src_device, int64_t bytes, void *stream);
+/* Non-blocking stream at the default priority; destroy NULL is a no-op.
+ * The reference has no stream concept (one DeviceContext per call,
+ * runtime.mojo:556). */
+int32_t mj_stream_create(void **stream);
+int32_t mj_stream_destroy(void *stream);
+/* Waits for all work on the device (DeviceContext.synchronize,
+ * runtime.mojo:596). */
+int32_t mj_device_synchronize(void);
+
+/* ---- host-pointer variants (api_host.hip) -------------------------------- */
+/* Same arguments and results as the device entry point without the `_h`
+ * suffix, with every pointer a HOST pointer: inputs are copied to one device
+ * block, the operator runs, and outputs are copied back before the call
+ * returns (the reference seam's copy-in / copy-out contract,
+ * tensor/gpu/runtime.mojo:556-604).  Strided operands are copied over the
+ * extent their strides span; outputs with a leading dimension are written
+ * row by row, leaving padding untouched.  This is what a momijo Tensor[T],
+ * whose storage is a host List[T] (tensor/tensor.mojo:776-905), binds. */
+
+/* Tensor.matmul / tensor.matmul Float32 (tensor/tensor.mojo:3168-3169,
+ * tensor/__init__.mojo:123 -> matmul_core_mm, tensor/broadcast.mojo:
+ * 1612-1673), with the tensor's _strides. */
+int32_t mj_matmul_f32_h(int64_t M, int64_t N, int64_t K,
+                        const float *A, int64_t sAm, int64_t sAk,
+                        const float *B, int64_t sBk, int64_t sBn,
+                        const float *bias, int32_t epilogue, float *C, int64_t ldc);
+/* Tensor.matmul_vec Float32 (tensor/tensor.mojo:3180 -> matmul_core_vec,
+ * tensor/broadcast.mojo:1543-1608). */
+int32_t mj_matvec_f32_h(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
+                        const float *x, int64_t sx, float *y);
+/* Float64 matmul / matmul2d (tensor/broadcast.mojo:1466-1538,
+ * tensor/math.mojo:7838-7880). */
+int32_t mj_matmul_f64_h(int64_t M, int64_t N, int64_t K,
+                        const double *A, int64_t sAm, int64_t sAk,
+                        const double *B, int64_t sBk, int64_t sBn, double *C, int64_t ldc);
+/* Float64 matmul_core_vec (tensor/broadcast.mojo:1397-1464). */
+int32_t mj_matvec_f64_h(int64_t M, int64_t N, const double *A, int64_t sAm, int64_t sAn,
+                        const double *x, int64_t sx, double *y);
+/* tensordot(A, B, axes=1) Float32 (tensor/broadcast.mojo:1694-1900). */
+int32_t mj_tensordot_f32_h(int32_t batch_rank, const int64_t *batch_shape,
+                           const int64_t *a_batch_strides, const int64_t *b_batch_strides,
+                           int64_t M, int64_t N, int64_t K,
+                           const float *A, int64_t sAm, int64_t sAk,
+                           const float *B, int64_t sBk, int64_t sBn, float *C);
+/* Linear.forward (learn/nn/layers.mojo:383-433, 510-516) + fused activation. */
+int32_t mj_linear_f32_h(const float *x, const float *W, const float *bias, int32_t epilogue,
+                        float *y, int64_t N, int64_t InF, int64_t OutF);
+/* Linear.backward (learn/nn/layers.mojo:519-618, 785-787). */
+int32_t mj_linear_backward_f32_h(const float *x, const float *W, const float *dy, float *dW,
+                                 float *db, float *dx, int64_t N, int64_t InF, int64_t OutF);
+/* The MATMUL2D tape rule in Float64 (tensor/autograd.mojo:1542-1555); with
+ * accumulate != 0 dA / dB are read as well as written. */
+int32_t mj_matmul_backward_f64_h(int64_t M, int64_t N, int64_t K, const double *A,
+                                 const double *B, const double *G, double *dA, double *dB,
+                                 int32_t accumulate);
+/* Tensor.relu / gelu / silu (tensor/tensor.mojo:3848,4003,4020). */
+int32_t mj_activation_f32_h(int32_t epilogue, const float *x, float *y, int64_t n);
+/* bf16 NT GEMM (no reference counterpart; see mj_gemm_bf16_nt). */
+int32_t mj_gemm_bf16_nt_h(int64_t M, int64_t N, int64_t K,
+                          const uint16_t *A, int64_t lda, const uint16_t *B, int64_t ldb,
+                          const float *bias, int32_t epilogue, uint16_t *C, int64_t ldc);
+/* quantize_symmetric_int8 (learn/api/functional.mojo:231-247). */
+int32_t mj_quantize_symmetric_int8_h(const float *x, int64_t n, float scale, int8_t *q);
+/* MinMaxObserver.observe reduction (learn/api/sequential.mojo:232-250);
+ * minmax_out is host float[2]. */
+int32_t mj_minmax_f32_h(const float *x, int64_t n, float *minmax_out);
+/* MinMaxObserver.observe + scale_symmetric (learn/api/sequential.mojo:
+ * 232-263); scale_out is a host float. */
+int32_t mj_minmax_scale_symmetric_h(const float *x, int64_t n, float max_q, float *scale_out);
+/* matmul_i8_i8_to_i32 (learn/api/functional.mojo:249-279). */
+int32_t mj_matmul_i8_i8_to_i32_h(const int8_t *A, const int8_t *B, int32_t *C,
+                                 int64_t M, int64_t N, int64_t K, int32_t legacy_literal);
+/* dequantize_i32_to_f32_add_bias (learn/api/functional.mojo:281-302). */
+int32_t mj_dequantize_i32_to_f32_add_bias_h(const int32_t *acc, float sf, const float *b,
+                                            float *y, int64_t M, int64_t N);
+/* QuantLinear.forward (learn/nn/layers.mojo:1681-1685). */
+int32_t mj_quant_linear_f32_h(const float *x, const int8_t *Wq, const float *b,
+                              float s_w, float s_x, float *y,
+                              int64_t M, int64_t N, int64_t K, int32_t legacy_literal);
+/* Per-row quantize/pack (generalises quantize_symmetric_int8 + convert,
+ * learn/api/sequential.mojo:436-450). */
+int32_t mj_quantize_rowwise_i8_h(const float *W, int64_t N, int64_t K, int32_t rounding,
+                                 int8_t *Q, float *scales);
+/* W8A16 Linear (no reference counterpart; see mj_linear_w8a16). */
+int32_t mj_linear_w8a16_h(const uint16_t *x, const int8_t *Q, const float *scales,
+                          const float *bias, int32_t epilogue, uint16_t *y,
+                          int64_t M, int64_t N, int64_t K);
+/* W8A16 FFN (no reference counterpart; see mj_mlp_w8a16); h may be NULL,
+ * then the intermediate stays on the device. */
+int32_t mj_mlp_w8a16_h(const uint16_t *x, const int8_t *Wg, const float *sg,
+                       const int8_t *Wu, const float *su, const int8_t *Wd, const float *sd,
+                       uint16_t *h, uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,36 @@ SIGNATURES = {
     "mj_quantize_rowwise_i8": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
     "mj_linear_w8a16": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _P]),
     "mj_mlp_w8a16": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    # device memory and streams
+    "mj_malloc": (_I32, [ctypes.POINTER(_P), _I64]),
+    "mj_free": (_I32, [_P]),
+    "mj_memcpy_htod": (_I32, [_P, _P, _I64, _P]),
+    "mj_memcpy_dtoh": (_I32, [_P, _P, _I64, _P]),
+    "mj_memcpy_dtod": (_I32, [_P, _P, _I64, _P]),
+    "mj_stream_create": (_I32, [ctypes.POINTER(_P)]),
+    "mj_stream_destroy": (_I32, [_P]),
+    "mj_device_synchronize": (_I32, []),
+    # host-pointer variants
+    "mj_matmul_f32_h": (_I32, [_I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64]),
+    "mj_matvec_f32_h": (_I32, [_I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "mj_matmul_f64_h": (_I32, [_I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64]),
+    "mj_matvec_f64_h": (_I32, [_I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "mj_tensordot_f32_h": (_I32, [_I32, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64,
+                                  _I64, _P]),
+    "mj_linear_f32_h": (_I32, [_P, _P, _P, _I32, _P, _I64, _I64, _I64]),
+    "mj_linear_backward_f32_h": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
+    "mj_matmul_backward_f64_h": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32]),
+    "mj_activation_f32_h": (_I32, [_I32, _P, _P, _I64]),
+    "mj_gemm_bf16_nt_h": (_I32, [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I32, _P, _I64]),
+    "mj_quantize_symmetric_int8_h": (_I32, [_P, _I64, _F, _P]),
+    "mj_minmax_f32_h": (_I32, [_P, _I64, _P]),
+    "mj_minmax_scale_symmetric_h": (_I32, [_P, _I64, _F, _P]),
+    "mj_matmul_i8_i8_to_i32_h": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I32]),
+    "mj_dequantize_i32_to_f32_add_bias_h": (_I32, [_P, _F, _P, _P, _I64, _I64]),
+    "mj_quant_linear_f32_h": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32]),
+    "mj_quantize_rowwise_i8_h": (_I32, [_P, _I64, _I64, _I32, _P, _P]),
+    "mj_linear_w8a16_h": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64]),
+    "mj_mlp_w8a16_h": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
 }
 
 _lib = None

@@ -4,45 +4,16 @@
 // per-thread message from mj_last_error().
 #include <hip/hip_runtime.h>
 
-#include <cstdarg>
-#include <cstdio>
 #include <cstring>
 
 #include "../../include/momijo_hip.h"
 #include "launch.h"
 
+#include "abi_util.h"
+
 namespace {
 
-thread_local char g_err[512] = "";
-
-int32_t fail(int32_t code, const char *fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int32_t hip_status(hipError_t e, const char *what) {
-  if (e == hipSuccess) return MJ_OK;
-  return fail(MJ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
-}
-
-bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
-
-bool valid_epi(int32_t e) { return e >= MJ_EPI_NONE && e <= MJ_EPI_RELU_UNARY; }
-
-constexpr int64_t kMaxDim = (int64_t)1 << 31;
-
-int32_t check_dims(int64_t M, int64_t N, int64_t K) {
-  if (M < 0 || N < 0 || K < 0) return fail(MJ_ERR_ARG, "negative size (M=%lld N=%lld K=%lld)",
-                                           (long long)M, (long long)N, (long long)K);
-  if (M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
-    return fail(MJ_ERR_UNSUPPORTED, "dimension exceeds 2^31");
-  return MJ_OK;
-}
-
-hipStream_t S(void *stream) { return (hipStream_t)stream; }
+using namespace mj_abi;
 
 // Plans and launches an NT GEMM, with a stream-ordered fp32 workspace when the
 // plan splits K.
@@ -81,46 +52,6 @@ int32_t run_colsum(const float *dy, int64_t N, int64_t OutF, float *db, hipStrea
   const int32_t st =
       hip_status(mj::launch_colsum_f32(dy, N, OutF, db, part, segs, stream), "colsum launch");
   if (part) (void)hipFreeAsync(part, stream);
-  return st;
-}
-
-// Device staging for the host-buffer seams: one device block holds a copy of
-// each of the n arrays; those with `host` set are copied in, `body` runs on
-// the null stream, and those with `host_out` set are copied back.
-struct HostArg {
-  const void *host;
-  void *host_out;
-  size_t bytes;
-};
-
-template <typename Body>
-int32_t with_device_copies(HostArg *args, int n, Body body) {
-  constexpr int kMaxArgs = 8;
-  if (n > kMaxArgs) return fail(MJ_ERR_ARG, "too many staged arrays");
-  size_t total = 0;
-  for (int i = 0; i < n; ++i) total += (args[i].bytes + 255) & ~(size_t)255;
-  char *dev = nullptr;
-  if (total && hipMalloc((void **)&dev, total) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "hipMalloc(%zu) failed", total);
-  }
-  void *d[kMaxArgs];
-  size_t off = 0;
-  int32_t st = MJ_OK;
-  for (int i = 0; i < n; ++i) {
-    d[i] = dev + off;
-    off += (args[i].bytes + 255) & ~(size_t)255;
-    if (!st && args[i].host && args[i].bytes)
-      st = hip_status(hipMemcpy(d[i], args[i].host, args[i].bytes, hipMemcpyHostToDevice),
-                      "copy in");
-  }
-  if (!st) st = body(d);
-  if (!st) st = hip_status(hipStreamSynchronize(nullptr), "device run");
-  for (int i = 0; i < n && !st; ++i)
-    if (args[i].host_out && args[i].bytes)
-      st = hip_status(hipMemcpy(args[i].host_out, d[i], args[i].bytes, hipMemcpyDeviceToHost),
-                      "copy out");
-  if (dev) (void)hipFree(dev);
   return st;
 }
 
