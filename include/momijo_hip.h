@@ -136,6 +136,16 @@ int32_t mj_matmul_backward_f64(int64_t M, int64_t N, int64_t K, const double *A,
                                const double *G, double *dA, double *dB, int32_t accumulate,
                                void *stream);
 
+/* The same MATMUL2D rule in Float32, the value type of the reference tape
+ * (Tape.values / grads are List[Tensor[Float32]], tensor/autograd.mojo:
+ * 214-216; GradTensor.matmul / matmul2d record the node, :930-939 and
+ * :995-1017): dA (+)= G @ B^T, dB (+)= A^T @ G on the fp32 MFMA engine, the
+ * products summed in fp32 and added to the old gradient with one rounding
+ * (grads[p].add(g)).  Either output may be NULL. */
+int32_t mj_matmul_backward_f32(int64_t M, int64_t N, int64_t K, const float *A, const float *B,
+                               const float *G, float *dA, float *dB, int32_t accumulate,
+                               void *stream);
+
 /* Host-pointer seam with the signature of launch_1d_linear_fw
  * (tensor/gpu/runtime.mojo:539-631): x [N,InF], wT [InF,OutF] (the layout
  * Linear.forward_gpu builds, layers.mojo:489-497), b [OutF], y [N,OutF];
@@ -327,6 +337,10 @@ int32_t mj_linear_backward_f32_h(const float *x, const float *W, const float *dy
  * accumulate != 0 dA / dB are read as well as written. */
 int32_t mj_matmul_backward_f64_h(int64_t M, int64_t N, int64_t K, const double *A,
                                  const double *B, const double *G, double *dA, double *dB,
+                                 int32_t accumulate);
+/* The MATMUL2D tape rule in Float32 (tensor/autograd.mojo:1542-1555). */
+int32_t mj_matmul_backward_f32_h(int64_t M, int64_t N, int64_t K, const float *A,
+                                 const float *B, const float *G, float *dA, float *dB,
                                  int32_t accumulate);
 /* Tensor.relu / gelu / silu (tensor/tensor.mojo:3848,4003,4020). */
 int32_t mj_activation_f32_h(int32_t epilogue, const float *x, float *y, int64_t n);

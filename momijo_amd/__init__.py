@@ -12,7 +12,8 @@ from ._lib import (EPI_GELU_TANH, EPI_GELU_TANH_APPROX, EPI_NONE, EPI_RELU, EPI_
 from .tensor import (Tensor, empty_f32, empty_f64, gemm_bf16_nt, gpu_available, matmul, matmul2d,
                      matmul_backward, tensordot)
 from .nn import Linear, QuantLinear, ReLU, W8Linear, W8MLP, quantize_rowwise_int8
-from . import seam, weights
+from . import autograd, seam, weights
+from .autograd import GradContext, GradTensor
 from .functional import (MinMaxObserver, convert, dequantize_i32_to_f32_add_bias,
                          matmul_i8_i8_to_i32, prepare, quantize_symmetric_int8)
 
@@ -23,6 +24,7 @@ __all__ = [
     "Linear", "ReLU", "QuantLinear", "W8Linear", "W8MLP", "quantize_rowwise_int8",
     "quantize_symmetric_int8", "matmul_i8_i8_to_i32", "dequantize_i32_to_f32_add_bias",
     "MinMaxObserver", "prepare", "convert", "MomijoHipError", "seam", "weights",
+    "autograd", "GradContext", "GradTensor",
     "EPI_NONE", "EPI_RELU", "EPI_GELU_TANH", "EPI_SILU", "EPI_GELU_TANH_APPROX",
     "EPI_SILU_APPROX", "EPI_RELU_UNARY", "ROUND_RHE", "ROUND_LEGACY",
 ]

@@ -58,6 +58,7 @@ SIGNATURES = {
     "mj_launch_linear_bw_dw_h": (_I32, [_P, _P, _P, _I64, _I64, _I64]),
     "mj_launch_linear_bw_db_h": (_I32, [_P, _P, _I64, _I64]),
     "mj_matmul_backward_f64": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P]),
+    "mj_matmul_backward_f32": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P]),
     "mj_activation_f32": (_I32, [_I32, _P, _P, _I64, _P]),
     "mj_gemm_bf16_nt": (_I32, [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I32, _P, _I64, _P]),
     "mj_quantize_symmetric_int8": (_I32, [_P, _I64, _F, _P, _P]),
@@ -88,6 +89,7 @@ SIGNATURES = {
     "mj_linear_f32_h": (_I32, [_P, _P, _P, _I32, _P, _I64, _I64, _I64]),
     "mj_linear_backward_f32_h": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "mj_matmul_backward_f64_h": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32]),
+    "mj_matmul_backward_f32_h": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32]),
     "mj_activation_f32_h": (_I32, [_I32, _P, _P, _I64]),
     "mj_gemm_bf16_nt_h": (_I32, [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I32, _P, _I64]),
     "mj_quantize_symmetric_int8_h": (_I32, [_P, _I64, _F, _P]),

@@ -283,6 +283,31 @@ int32_t mj_matmul_backward_f64(int64_t M, int64_t N, int64_t K, const double *A,
   return MJ_OK;
 }
 
+int32_t mj_matmul_backward_f32(int64_t M, int64_t N, int64_t K, const float *A, const float *B,
+                               const float *G, float *dA, float *dB, int32_t accumulate,
+                               void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  const bool want_dA = dA && M > 0 && K > 0;
+  const bool want_dB = dB && K > 0 && N > 0;
+  if ((want_dA || want_dB) && N > 0 && M > 0 && !G) return fail(MJ_ERR_ARG, "null G");
+  if (want_dA && N > 0 && !B) return fail(MJ_ERR_ARG, "null B");
+  if (want_dB && M > 0 && !A) return fail(MJ_ERR_ARG, "null A");
+  const int accum = accumulate ? 1 : 0;
+  const hipStream_t st = S(stream);
+  // dA [M, K] (+)= G [M, N] @ B^T: B^T is the view (row stride 1, column stride N) of B [K, N]
+  if (want_dA) {
+    if (int32_t e = hip_status(
+            mj::launch_gemm_f32_accum(M, K, N, G, N, 1, B, 1, N, dA, K, accum, st),
+            "matmul backward dA"))
+      return e;
+  }
+  // dB [K, N] (+)= A^T @ G: A^T is the view (row stride 1, column stride K) of A [M, K]
+  if (want_dB)
+    return hip_status(mj::launch_gemm_f32_accum(K, N, M, A, 1, K, G, N, 1, dB, N, accum, st),
+                      "matmul backward dB");
+  return MJ_OK;
+}
+
 int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream) {
   if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
   if (n < 0) return fail(MJ_ERR_ARG, "negative size");

@@ -267,6 +267,30 @@ int32_t mj_matmul_backward_f64_h(int64_t M, int64_t N, int64_t K, const double *
   });
 }
 
+int32_t mj_matmul_backward_f32_h(int64_t M, int64_t N, int64_t K, const float *A,
+                                 const float *B, const float *G, float *dA, float *dB,
+                                 int32_t accumulate) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  const bool want_dA = dA && M > 0 && K > 0;
+  const bool want_dB = dB && K > 0 && N > 0;
+  if ((want_dA || want_dB) && N > 0 && M > 0 && !G) return fail(MJ_ERR_ARG, "null G");
+  if (want_dA && N > 0 && !B) return fail(MJ_ERR_ARG, "null B");
+  if (want_dB && M > 0 && !A) return fail(MJ_ERR_ARG, "null A");
+  if (!want_dA && !want_dB) return MJ_OK;
+  HostArg a[5] = {{want_dB ? A : nullptr, nullptr, want_dB ? (size_t)(M * K) * F4 : 0},
+                  {want_dA ? B : nullptr, nullptr, want_dA ? (size_t)(K * N) * F4 : 0},
+                  {G, nullptr, (size_t)(M * N) * F4},
+                  {want_dA && accumulate ? dA : nullptr, want_dA ? dA : nullptr,
+                   want_dA ? (size_t)(M * K) * F4 : 0},
+                  {want_dB && accumulate ? dB : nullptr, want_dB ? dB : nullptr,
+                   want_dB ? (size_t)(K * N) * F4 : 0}};
+  return with_device_copies(a, 5, [&](void **d) {
+    return mj_matmul_backward_f32(M, N, K, (const float *)d[0], (const float *)d[1],
+                                  (const float *)d[2], (float *)d[3], (float *)d[4], accumulate,
+                                  nullptr);
+  });
+}
+
 int32_t mj_activation_f32_h(int32_t epilogue, const float *x, float *y, int64_t n) {
   if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
   if (n < 0) return fail(MJ_ERR_ARG, "negative size");

@@ -227,6 +227,13 @@ hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int6
                           1, stream);
 }
 
+hipError_t launch_gemm_f32_accum(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                                 int64_t sAk, const float *B, int64_t sBk, int64_t sBn, float *C,
+                                 int64_t ldc, int accum, hipStream_t stream) {
+  return launch_fx<float>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, accum, C, ldc,
+                          BatchDesc{}, 1, stream);
+}
+
 hipError_t launch_gemm_f32_batched(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
                                    int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                                    float *C, const BatchDesc &bd, int64_t batches,

@@ -74,6 +74,11 @@ hipError_t launch_gemm_f32(int64_t M, int64_t N, int64_t K, const float *A, int6
                            int64_t sAk, const float *B, int64_t sBk, int64_t sBn,
                            const float *bias, int epi, float *C, int64_t ldc,
                            hipStream_t stream);
+// C = A @ B, or with accum C = C + A @ B (one rounding of the fp32 product
+// sum onto the old value: the tape's grads[p].add(g)).
+hipError_t launch_gemm_f32_accum(int64_t M, int64_t N, int64_t K, const float *A, int64_t sAm,
+                                 int64_t sAk, const float *B, int64_t sBk, int64_t sBn, float *C,
+                                 int64_t ldc, int accum, hipStream_t stream);
 hipError_t launch_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, int64_t sAn,
                              const float *x, int64_t sx, float *y, hipStream_t stream);
 hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,

@@ -119,10 +119,12 @@ class Tensor:
         return matmul(self, other)
 
     def matmul_vec(self, x: "Tensor") -> "Tensor":
-        """Tensor.matmul_vec (tensor/tensor.mojo:3180-3181)."""
-        if self._t.dim() != 2 or x._t.dim() != 1 or x._t.shape[0] != self._t.shape[1]:
-            return empty_f64() if self._t.dtype == torch.float64 else empty_f32()
-        return _matvec(self, x)
+        """Tensor.matmul_vec (tensor/tensor.mojo:3167-3181); Tensor[Int]
+        operands are upcast to Float32 first (:3174-3178)."""
+        a, v = _upcast_int_pair(self, x)
+        if a._t.dim() != 2 or v._t.dim() != 1 or v._t.shape[0] != a._t.shape[1]:
+            return empty_f64() if a._t.dtype == torch.float64 else empty_f32()
+        return _matvec(a, v)
 
     # ---------------------------------------------------------------- unary
     def _unary(self, epi: int) -> "Tensor":
@@ -169,6 +171,19 @@ def empty_f64() -> Tensor:
     return Tensor(torch.empty(0, dtype=torch.float64, device=_device()))
 
 
+_INT_DTYPES = (torch.int64, torch.int32)
+
+
+def _upcast_int_pair(A: Tensor, B: Tensor) -> tuple[Tensor, Tensor]:
+    """Tensor[Int] @ Tensor[Int] -> Float32: both operands are converted with
+    astype_f32_from_int (tensor/tensor.mojo:3161-3165, 3174-3178: a
+    round-to-nearest Float32(Int) cast, here torch's int-to-float cast on the
+    device), then the Float32 product runs.  Other dtypes pass through."""
+    if A._t.dtype in _INT_DTYPES and B._t.dtype in _INT_DTYPES:
+        return Tensor(A._t.to(torch.float32)), Tensor(B._t.to(torch.float32))
+    return A, B
+
+
 def _matvec(A: Tensor, x: Tensor) -> Tensor:
     a, v = A._t, x._t
     M, N = a.shape
@@ -185,7 +200,9 @@ def matmul(A: Tensor, B: Tensor) -> Tensor:
 
     Float32 operands run the fp32 engine with their strides (transposed views
     need no copy).  bfloat16 operands run the bf16 MFMA GEMM, which takes B as
-    the transpose view of a row-major [N, K] weight (x.matmul(W.transpose()))."""
+    the transpose view of a row-major [N, K] weight (x.matmul(W.transpose())).
+    Tensor[Int] operands are upcast to Float32 (tensor/tensor.mojo:3161-3165)."""
+    A, B = _upcast_int_pair(A, B)
     a, b = A._t, B._t
     empty = empty_f64 if a.dtype == torch.float64 else empty_f32
     if a.dim() == 2 and b.dim() == 1:

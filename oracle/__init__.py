@@ -105,6 +105,7 @@ def _declare(L):
         "mo_tensordot_f32": (None, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64]),
         "mo_linear_backward_f32": (None, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
         "mo_matmul_backward_f64": (None, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
+        "mo_matmul_backward_f32": (None, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -230,6 +231,23 @@ def matmul_backward_f64(a, b, g, da=None, db=None):
     oa = _c(da, np.float64).copy() if da is not None else np.zeros((M, K))
     ob = _c(db, np.float64).copy() if db is not None else np.zeros((K, N))
     lib().mo_matmul_backward_f64(_ptr(a), _ptr(b), _ptr(g), _ptr(oa), _ptr(ob), M, N, K, acc)
+    return oa, ob
+
+
+def matmul_backward_f32(a, b, g, da=None, db=None):
+    """The MATMUL2D rule with the tape's Float32 values (tensor/autograd.mojo:
+    214-216, 1542-1555): returns (da + g @ b^T, db + a^T @ g), each product
+    in strict inner order; with da/db None the sums start from zero."""
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    g = _c(g, np.float32)
+    M, K = a.shape
+    N = b.shape[1]
+    assert b.shape == (K, N) and g.shape == (M, N)
+    acc = 1 if (da is not None or db is not None) else 0
+    oa = _c(da, np.float32).copy() if da is not None else np.zeros((M, K), np.float32)
+    ob = _c(db, np.float32).copy() if db is not None else np.zeros((K, N), np.float32)
+    lib().mo_matmul_backward_f32(_ptr(a), _ptr(b), _ptr(g), _ptr(oa), _ptr(ob), M, N, K, acc)
     return oa, ob
 
 

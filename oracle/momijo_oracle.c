@@ -667,3 +667,27 @@ MO_API void mo_matmul_backward_f64(const double *a, const double *b, const doubl
                 db[k * N + j] = accumulate ? db[k * N + j] + acc : acc;
             }
 }
+
+/* The MATMUL2D tape rule with Float32 values and gradients (the tape's type,
+ * tensor/autograd.mojo:214-216; rule :1542-1555): ga = g_out @ b^T and
+ * gb = a^T @ g_out as the Float32 matmul computes them (matmul_core_mm,
+ * tensor/broadcast.mojo:1620-1645: strict ascending inner index, one rounding
+ * per multiply and per add), then grads[p] = grads[p].add(g): one rounding
+ * of old + g. */
+MO_API void mo_matmul_backward_f32(const float *a, const float *b, const float *g, float *da,
+                                   float *db, int64_t M, int64_t N, int64_t K, int accumulate) {
+    if (da)
+        for (int64_t i = 0; i < M; ++i)
+            for (int64_t k = 0; k < K; ++k) {
+                float acc = 0.0f;
+                for (int64_t j = 0; j < N; ++j) acc = acc + g[i * N + j] * b[k * N + j];
+                da[i * K + k] = accumulate ? da[i * K + k] + acc : acc;
+            }
+    if (db)
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t j = 0; j < N; ++j) {
+                float acc = 0.0f;
+                for (int64_t i = 0; i < M; ++i) acc = acc + a[i * K + k] * g[i * N + j];
+                db[k * N + j] = accumulate ? db[k * N + j] + acc : acc;
+            }
+}

@@ -102,3 +102,51 @@ def test_matmul_backward_accumulates(oracle):
     da, db = oracle.matmul_backward_f64(a, b, g, ga0, gb0)
     np.testing.assert_array_equal(da, ga0 + g @ b.T)
     np.testing.assert_array_equal(db, gb0 + a.T @ g)
+
+
+# ------------------------------------------------------------- Float32 tape rule
+def test_matmul_backward_f32_integer_exact(oracle):
+    """Integer-valued operands: every product and partial sum is exact in
+    fp32, so da = g b^T and db = a^T g must equal the int64 products; a
+    swapped or untransposed operand would fail (the shapes are all distinct)."""
+    rng = np.random.default_rng(31)
+    M, K, N = 7, 5, 9
+    a = rng.integers(-6, 7, size=(M, K)).astype(np.float32)
+    b = rng.integers(-6, 7, size=(K, N)).astype(np.float32)
+    g = rng.integers(-6, 7, size=(M, N)).astype(np.float32)
+    da, db = oracle.matmul_backward_f32(a, b, g)
+    ai, bi, gi = (t.astype(np.int64) for t in (a, b, g))
+    np.testing.assert_array_equal(da, gi @ bi.T)
+    np.testing.assert_array_equal(db, ai.T @ gi)
+
+
+def test_matmul_backward_f32_strict_order(oracle):
+    """The Float32 products are summed in ascending inner index with one
+    rounding per step, as the Float32 matmul does; the accumulated form adds
+    the rounded sum onto the old gradient with one more rounding."""
+    rng = np.random.default_rng(32)
+    M, K, N = 4, 3, 37
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    g = rng.standard_normal((M, N)).astype(np.float32)
+    ga0 = rng.standard_normal((M, K)).astype(np.float32)
+    da, _ = oracle.matmul_backward_f32(a, b, g, ga0, None)
+    for i in range(M):
+        for k in range(K):
+            acc = np.float32(0)
+            for j in range(N):
+                acc = np.float32(acc + np.float32(g[i, j] * b[k, j]))
+            assert da[i, k] == np.float32(ga0[i, k] + acc)
+
+
+def test_matmul_backward_f32_directional_derivative(oracle):
+    """For L = <g, a @ b>: dL/da . E = <g, E @ b> and dL/db . F = <g, a @ F>
+    (fp64 closed forms)."""
+    rng = np.random.default_rng(33)
+    M, K, N = 16, 24, 12
+    a, b, g = (rng.standard_normal(s).astype(np.float32) for s in ((M, K), (K, N), (M, N)))
+    E, F = rng.standard_normal((M, K)), rng.standard_normal((K, N))
+    da, db = oracle.matmul_backward_f32(a, b, g)
+    a64, b64, g64 = (t.astype(np.float64) for t in (a, b, g))
+    np.testing.assert_allclose(np.sum(da * E), np.sum(g64 * (E @ b64)), rtol=1e-5)
+    np.testing.assert_allclose(np.sum(db * F), np.sum(g64 * (a64 @ F)), rtol=1e-5)
