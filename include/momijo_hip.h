@@ -235,6 +235,19 @@ int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b,
                             int64_t M, int64_t N, int64_t K, int32_t legacy_literal,
                             void *stream);
 
+/* mj_quant_linear_f32 without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The int8
+ * copy of x lives in a static 16 MiB device array owned by the library (one
+ * per GPU, held until the process ends), so M*K must be at most 16 MiB - 16
+ * bytes (MJ_ERR_UNSUPPORTED otherwise).  Results equal mj_quant_linear_f32's.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or host threads without ordering) race. */
+int32_t mj_quant_linear_f32_noalloc(const float *x, const int8_t *Wq, const float *b,
+                                    float s_w, float s_x, float *y,
+                                    int64_t M, int64_t N, int64_t K, int32_t legacy_literal,
+                                    void *stream);
+
 /* ---- int8: per-output-channel weight-only (BASELINE spec) -------------- */
 
 /* Q[N,K] int8 and scales[N] from W[N,K] fp32, one scale per output row.

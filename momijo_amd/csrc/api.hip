@@ -11,9 +11,48 @@
 
 #include "abi_util.h"
 
+#include <atomic>
+#include <mutex>
+
+// Scratch of mj_quant_linear_f32_noalloc: the int8 copy of x lives in this
+// file-scope device array instead of a per-call allocation.  Each GPU holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: the array is used only through the
+// per-device address that hipGetSymbolAddress returns (noalloc_scratch).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 using namespace mj_abi;
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+int32_t noalloc_scratch(int8_t **out) {
+  int dev = 0;
+  if (int32_t st = hip_status(hipGetDevice(&dev), "hipGetDevice")) return st;
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(MJ_ERR_UNSUPPORTED, "device %d is beyond the %d devices the scratch table holds",
+                dev, kMaxScratchDevices);
+  void *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (int32_t st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                                  "hipGetSymbolAddress(scratch)"))
+        return st;
+      if (!p) return fail(MJ_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = (int8_t *)p;
+  return MJ_OK;
+}
 
 // Plans and launches an NT GEMM, with a stream-ordered fp32 workspace when the
 // plan splits K.
@@ -36,6 +75,29 @@ int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
   int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
   if (ws) (void)hipFreeAsync(p.part, stream);
   return st;
+}
+
+// QuantLinear.forward on a caller-provided int8 buffer xq of M*K bytes
+// (16-byte aligned): quantize x with s_x, then the int8 GEMM with the
+// dequantize fused.  Every byte of xq that the GEMM reads is written by the
+// quantize first, so the buffer needs no clearing.
+int32_t quant_linear_body(const float *x, const int8_t *Wq, const float *b, float s_w, float s_x,
+                          float *y, int64_t M, int64_t N, int64_t K, int32_t legacy_literal,
+                          int8_t *xq, hipStream_t stream) {
+  const bool fast = !legacy_literal && K % 16 == 0 && aligned16(Wq) && aligned16(xq);
+  int32_t st = MJ_OK;
+  if (M * K > 0)
+    st = hip_status(mj::launch_quantize_tensor_legacy(x, M * K, s_x, xq, stream),
+                    "quantize launch");
+  // sf = s_x * s_w with the reference's (unguarded) s_x (layers.mojo:1684)
+  const float sf = s_x * s_w;
+  if (st) return st;
+  if (fast)
+    return hip_status(mj::launch_gemm_i8(xq, Wq, nullptr, y, sf, b, M, N, K, stream),
+                      "gemm_i8 launch");
+  return hip_status(mj::launch_gemm_i8_scalar(xq, Wq, nullptr, y, sf, b, M, N, K,
+                                              legacy_literal != 0, stream),
+                    "gemm_i8 scalar launch");
 }
 
 // db = column sums of dy [N, OutF], with a stream-ordered workspace when the
@@ -401,30 +463,32 @@ int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, fl
   if (int32_t s = check_dims(M, N, K)) return s;
   if (M == 0 || N == 0) return MJ_OK;
   if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
-  const bool fast = !legacy_literal && K % 16 == 0 && aligned16(Wq);  // xq is allocated aligned
   int8_t *xq = nullptr;
   const size_t bytes = (size_t)M * K + 16;
   if (hipMallocAsync((void **)&xq, bytes, S(stream)) != hipSuccess) {
     (void)hipGetLastError();
     return fail(MJ_ERR_ALLOC, "workspace allocation failed");
   }
-  int32_t st = MJ_OK;
-  if (M * K > 0)
-    st = hip_status(mj::launch_quantize_tensor_legacy(x, M * K, s_x, xq, S(stream)),
-                    "quantize launch");
-  // sf = s_x * s_w with the reference's (unguarded) s_x (layers.mojo:1684)
-  const float sf = s_x * s_w;
-  if (!st) {
-    if (fast)
-      st = hip_status(mj::launch_gemm_i8(xq, Wq, nullptr, y, sf, b, M, N, K, S(stream)),
-                      "gemm_i8 launch");
-    else
-      st = hip_status(mj::launch_gemm_i8_scalar(xq, Wq, nullptr, y, sf, b, M, N, K,
-                                                legacy_literal != 0, S(stream)),
-                      "gemm_i8 scalar launch");
-  }
+  const int32_t st = quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq,
+                                       S(stream));
   (void)hipFreeAsync(xq, S(stream));
   return st;
+}
+
+int32_t mj_quant_linear_f32_noalloc(const float *x, const int8_t *Wq, const float *b, float s_w,
+                                    float s_x, float *y, int64_t M, int64_t N, int64_t K,
+                                    int32_t legacy_literal, void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
+  if ((uint64_t)M * (uint64_t)K + 16 > kNoAllocScratchBytes)
+    return fail(MJ_ERR_UNSUPPORTED,
+                "mj_quant_linear_f32_noalloc: the quantized x needs M*K = %lld bytes; the static "
+                "scratch holds %zu (use mj_quant_linear_f32)",
+                (long long)(M * K), kNoAllocScratchBytes - 16);
+  int8_t *xq = nullptr;
+  if (int32_t st = noalloc_scratch(&xq)) return st;
+  return quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq, S(stream));
 }
 
 // ------------------------------------------------------------------ int8 per-channel
