@@ -75,6 +75,7 @@ _U64 = ctypes.c_uint64
 def _declare(L):
     sig = {
         "mo_rng_words": (None, [_U64, _P, _I64]),
+        "mo_rng_words_from_state": (None, [_U64, _U64, _P, _I64]),
         "mo_randu_f32": (None, [_P, _I64, _D, _D, _U64]),
         "mo_randn_f32": (None, [_P, _I64, _D, _D, _U64]),
         "mo_randn_f32_f32core": (None, [_P, _I64, _U64]),
@@ -128,6 +129,13 @@ def _c(a, dtype):
 def rng_words(seed: int, n: int) -> np.ndarray:
     out = np.empty(n, np.uint64)
     lib().mo_rng_words(seed, _ptr(out), n)
+    return out
+
+
+def rng_words_from_state(s0: int, s1: int, n: int) -> np.ndarray:
+    """n raw xoroshiro128** words from the state (s0, s1) (no seeding)."""
+    out = np.empty(n, np.uint64)
+    lib().mo_rng_words_from_state(s0, s1, _ptr(out), n)
     return out
 
 

@@ -101,6 +101,13 @@ MO_API void mo_rng_words(uint64_t seed, uint64_t *out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = mo_rng_next_u64(&r);
 }
 
+/* Raw words from an explicit state (s0, s1), without the splitmix64 seeding:
+ * for known-answer checks of the xoroshiro128** step itself. */
+MO_API void mo_rng_words_from_state(uint64_t s0, uint64_t s1, uint64_t *out, int64_t n) {
+    mo_rng r; r.s0 = s0; r.s1 = s1;
+    for (int64_t i = 0; i < n; ++i) out[i] = mo_rng_next_u64(&r);
+}
+
 /* randu_with[Float32] (creation.mojo:495-526): f(low + (high-low)*next_f64)
  * with f = Float32(.) (tensor/cast.mojo:353-354). */
 MO_API void mo_randu_f32(float *out, int64_t n, double low, double high, uint64_t seed) {

@@ -2,9 +2,10 @@
 
 The checks are independent of the C code: a pure-Python restatement of
 Vigna's published splitmix64 and xoroshiro128** (with the reference's seed
-handling), the well-known first splitmix64 output for state 0, the
-uniform/normal mappings recomputed from raw words, and a committed golden
-vector of raw words.
+handling), the well-known first splitmix64 output for state 0, a published
+xoroshiro128** known-answer vector for an explicit state, the uniform/normal
+mappings recomputed from raw words, and a committed golden vector of raw
+words.
 """
 import json
 import math
@@ -52,6 +53,19 @@ def test_splitmix_known_first_output():
     # reference sequence of Vigna's splitmix64.c)
     _, z = _splitmix_next(0)
     assert z == 0xE220A8397B1DCDAF
+
+
+def test_xoroshiro128starstar_known_answer(oracle):
+    """The step of RNG64.next_u64 (creation.mojo:92-100) against a published
+    known-answer vector: the first ten outputs of xoroshiro128** from the
+    state s0 = 1, s1 = 2, as listed by the rand_xoshiro crate's reference test
+    for Xoroshiro128StarStar, which records them as produced with Vigna's
+    reference C implementation (xoroshiro128starstar.c).  A wrong rotation,
+    shift or multiplier changes every word after the first two."""
+    expected = [5760, 97769243520, 9706862127477703552, 9223447511460779954,
+                8358291023205304566, 15695619998649302768, 8517900938696309774,
+                16586480348202605369, 6959129367028440372, 16822147227405758281]
+    assert [int(v) for v in oracle.rng_words_from_state(1, 2, 10)] == expected
 
 
 def test_words_match_independent_restatement(oracle):
