@@ -12,7 +12,8 @@ import pytest
 import torch
 
 import momijo_amd as mj
-from _util import bf16_dev, bf16_host_bits, bf16_host_f32, normwise_rel, to_dev
+from _util import (assert_tiles_covered, bf16_dev, bf16_host_bits, bf16_host_f32,
+                   normwise_rel, slab_cols, slab_rows, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -233,15 +234,24 @@ def test_gemv_shapes(oracle, dev, M, N, K):
 
 
 def test_c4_prefill_gelu(oracle, dev):
+    """C4 at full size, every output tile checked at full K: one row in every
+    128-row block over all 4096 columns, two columns in every 256-wide block
+    over all 2048 rows."""
     M, N, K = 2048, 4096, 4096
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, 40)
     lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_GELU_TANH)
     y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    rows, cols = slab_rows(M), slab_cols(N)
     worst = 0.0
-    for r in (0, 1, 127, 128, 1023, 2046, 2047):
+    for r in rows:
         _, ref = oracle.linear_w8a16(x[r:r + 1], Q, s, b, mj.EPI_GELU_TANH)
         worst = max(worst, normwise_rel(y[r:r + 1], ref))
-    print(f"C4 prefill worst normwise rel err {worst:.3e}", flush=True)
+    _, ref_cols = oracle.linear_w8a16(x, np.ascontiguousarray(Q[cols]), s[cols], b[cols],
+                                      mj.EPI_GELU_TANH)
+    worst = max(worst, normwise_rel(y[:, cols], ref_cols))
+    assert_tiles_covered(M, N, rows, cols)
+    print(f"C4 prefill: {len(rows)} rows, {len(cols)} columns; worst normwise rel err "
+          f"{worst:.3e}", flush=True)
     assert worst <= BF16_TOL
 
 
@@ -345,15 +355,36 @@ def _run_mlp(dev, x, Wg, sg, Wu, su, Wd, sd):
 
 
 def test_c5_mlp(oracle, dev):
+    """C5 at full size, every tile of both GEMMs checked at full K:
+    - h = silu(x Wg^T) * (x Wu^T) and y on one row per 128-row block (all
+      11008 / 4096 columns) against the oracle's FFN;
+    - h on two columns per 256-wide block over all 512 rows (the oracle's FFN
+      restricted to those gate/up rows);
+    - y on two columns per 256-wide block over all rows, from the device's h
+      (checked above) through the oracle's W8A16 Linear: this pins every tile
+      and K slice of the down projection by itself."""
     M, K, I, H = 512, 4096, 11008, 4096
-    case = _mlp_case(oracle, M, K, I, H, 0)
+    x, Wg, sg, Wu, su, Wd, sd = case = _mlp_case(oracle, M, K, I, H, 0)
     y, h = _run_mlp(dev, *case)
+    rows = slab_rows(M)
     worst_h = worst_y = 0.0
-    for r in (0, 255, 256, 511):
+    for r in rows:
         hr, yr = oracle.mlp_w8a16(*case, rows=(r, r + 1))
         worst_h = max(worst_h, normwise_rel(h[r:r + 1], oracle.bf16_to_f32(hr)))
         worst_y = max(worst_y, normwise_rel(y[r:r + 1], oracle.bf16_to_f32(yr)))
-    print(f"C5 mlp worst normwise rel err h {worst_h:.3e} y {worst_y:.3e}", flush=True)
+    hc = slab_cols(I)
+    sub = (x, np.ascontiguousarray(Wg[hc]), sg[hc], np.ascontiguousarray(Wu[hc]), su[hc],
+           np.ascontiguousarray(Wd[:, hc]), sd)
+    hr_cols, _ = oracle.mlp_w8a16(*sub)
+    worst_h = max(worst_h, normwise_rel(h[:, hc], oracle.bf16_to_f32(hr_cols)))
+    yc = slab_cols(H)
+    h_bits = oracle.f32_to_bf16(h)              # h is bf16: this is exact
+    _, yr_cols = oracle.linear_w8a16(h_bits, np.ascontiguousarray(Wd[yc]), sd[yc])
+    worst_y = max(worst_y, normwise_rel(y[:, yc], yr_cols))
+    assert_tiles_covered(M, I, rows, hc)
+    assert_tiles_covered(M, H, rows, yc)
+    print(f"C5 mlp: {len(rows)} rows, {len(hc)} + {len(yc)} columns; worst normwise rel err "
+          f"h {worst_h:.3e} y {worst_y:.3e}", flush=True)
     assert worst_h <= BF16_TOL and worst_y <= BF16_TOL
 
 
