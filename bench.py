@@ -20,7 +20,9 @@ weights from HBM.
 
 ``cpu_baseline`` times the oracle (the C restatement of momijo's CPU tensor
 engine, single-threaded as the reference is) on a row slab of C2, on this
-box's host cores.
+box's host cores, using the very bytes the GPU leg multiplied (copied back
+from the device after its timed region; sha256 recorded).  The C3 and C1
+entries carry their own ``cpu_baseline``, timed in full the same way.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -111,6 +113,18 @@ def _rand_f32(shape, seed, std=1.0):
     return torch.randn(shape, generator=g, device="cuda") * std
 
 
+# Inputs of the GPU legs that the CPU baseline re-times on the same bytes
+# (copied from the device after the timed region): name -> host arrays.
+_CPU_INPUTS = {}
+
+
+def _host_bf16_bits(t):
+    """bf16 device tensor -> uint16 host array of its bit patterns."""
+    import numpy as np
+    import torch
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
 def bench_c2(steps, warmup):
     import momijo_amd as mj
     M = N = K = 4096
@@ -118,6 +132,8 @@ def bench_c2(steps, warmup):
     B = _rand_bf16((N, K), 2)
     C = mj.gemm_bf16_nt(A, B)
     ms = _time_launches(lambda i: mj.gemm_bf16_nt(A, B, out=C), steps, warmup)
+    # the CPU leg times the oracle on a row slab of these exact bytes
+    _CPU_INPUTS["c2"] = (_host_bf16_bits(A[:256]), _host_bf16_bits(B))
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     return {
@@ -189,6 +205,7 @@ def bench_c3(steps, warmup):
     floor_ms = _graph_ms_per_launch(lambda i: tiny.forward(x, out=y4), 64, 4)
     bytes_ = N * K + N * 4 + K * 2 + N * 4 + N * 2   # Q + scales + x + bias(f32) + y
     gbs = bytes_ / (ms * 1e-3) / 1e9
+    _CPU_INPUTS["c3"] = (_host_bf16_bits(x), q0.cpu().numpy(), s.cpu().numpy(), bias.cpu().numpy())
     return {
         "name": "c3_int8_gemv_11008x4096",
         "metric": "int8 weight-only GEMV GB/s (M=1)",
@@ -286,6 +303,8 @@ def bench_c1(steps, warmup):
     lin.weight.torch.copy_(_rand_f32((256, 256), 2))
     lin.bias_t.torch.copy_((torch.rand(256, device="cuda") - 0.5) / 8)
     ms = _time_launches(lambda i: lin.forward_act(x, mj.EPI_RELU), steps, warmup)
+    _CPU_INPUTS["c1"] = (x.torch.cpu().numpy(), lin.weight.torch.cpu().numpy(),
+                         lin.bias_t.torch.cpu().numpy())
     flops = 2.0 * 256 ** 3
     tf = flops / (ms * 1e-3) / 1e12
     return {
@@ -374,23 +393,85 @@ def bench_vendor(steps, warmup):
     return out
 
 
-def cpu_baseline_c2(rows: int = 256):
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _sha256(*arrays) -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(a.tobytes())
+    return h.hexdigest()
+
+
+def _time_cpu(fn, min_s: float):
+    """Seconds per call of fn(), repeated until min_s seconds have passed."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return dt / n, n
+
+
+def cpu_baseline_c2():
     """The oracle's strict-k fp32 dot on upcast bf16 inputs (momijo's CPU
-    engine applied to bf16 data, single thread) over `rows` rows of C2
-    (about 10 s of CPU work)."""
+    engine applied to bf16 data, single thread), on the first 256 rows of the
+    exact A and the full B the GPU leg multiplied (about 10 s of CPU work)."""
     import oracle
     oracle.build()
-    K = N = 4096
-    A = oracle.f32_to_bf16(oracle.randn_f32((rows, K), seed=1))
-    B = oracle.f32_to_bf16(oracle.randn_f32((N, K), seed=2))
+    A, B = _CPU_INPUTS["c2"]
+    rows = A.shape[0]
+    N, K = B.shape
     t0 = time.perf_counter()
     oracle.gemm_bf16_nt(A, B, rows=(0, rows))
     dt = time.perf_counter() - t0
     flops = 2.0 * rows * N * K
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"C2 row slab: {rows} of 4096 rows x N=4096 x K=4096 "
-                      f"({dt:.1f} s, oracle/momijo_oracle.c mo_gemm_bf16_nt, gcc -O2, 1 thread)",
-            "host_nproc": os.cpu_count()}
+            "sample": f"C2 row slab: rows 0..{rows - 1} of the GPU leg's A (4096 x 4096) times "
+                      f"its full B (N={N}, K={K}), the same bf16 bytes ({dt:.1f} s, "
+                      "oracle/momijo_oracle.c mo_gemm_bf16_nt, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(A, B), "host_nproc": os.cpu_count(),
+            "cpu_model": _cpu_model()}
+
+
+def cpu_baseline_c3():
+    """The W8A16 GEMV restated in the oracle (strict-k fp32 dot per row),
+    timed in full on the GPU leg's x, Q, scales and bias, single thread."""
+    import oracle
+    oracle.build()
+    x, Q, s, b = _CPU_INPUTS["c3"]
+    per_call, n = _time_cpu(lambda: oracle.linear_w8a16(x, Q, s, b), 2.0)
+    bytes_ = Q.size + s.nbytes + x.nbytes + b.nbytes + Q.shape[0] * 2
+    return {"value": bytes_ / per_call / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_call": per_call * 1e3,
+            "sample": f"full C3 (1 x {Q.shape[0]} x {Q.shape[1]}), {n} calls on the GPU leg's "
+                      "bytes (oracle mo_linear_w8a16, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(x, Q, s, b)}
+
+
+def cpu_baseline_c1():
+    """Linear(256 -> 256) + bias + ReLU as momijo's forward_cpu_parallel
+    computes it (oracle), in full, on the GPU leg's x, W and b."""
+    import oracle
+    oracle.build()
+    x, W, b = _CPU_INPUTS["c1"]
+    per_call, n = _time_cpu(lambda: oracle.linear_act_f32(x, W, b, oracle.EPI_RELU), 1.0)
+    return {"value": 2.0 * 256 ** 3 / per_call / 1e12, "unit": "TFLOP/s", "cores": 1,
+            "kind": "port", "ms_per_call": per_call * 1e3,
+            "sample": f"full C1 Linear+ReLU 256^3, {n} calls on the GPU leg's bytes "
+                      "(oracle mo_linear_act_f32, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(x, W, b)}
 
 
 def main():
@@ -428,9 +509,16 @@ def main():
     gpu_wall = time.perf_counter() - t0
 
     cpu = None
-    if not a.no_cpu and want("c2"):
-        cpu = cpu_baseline_c2()
-        print(f"# cpu baseline done: {cpu['value']:.2e} TFLOP/s", file=sys.stderr, flush=True)
+    if not a.no_cpu:
+        if "c2" in _CPU_INPUTS:
+            cpu = cpu_baseline_c2()
+            print(f"# cpu baseline done: {cpu['value']:.2e} TFLOP/s", file=sys.stderr, flush=True)
+        for key, fn in (("c3", cpu_baseline_c3), ("c1", cpu_baseline_c1)):
+            if key in _CPU_INPUTS:
+                entry = next(r for r in secondary if r["name"].startswith(key + "_"))
+                entry["cpu_baseline"] = fn()
+                print(f"# {key} cpu baseline done: {entry['cpu_baseline']['value']:.3g} "
+                      f"{entry['cpu_baseline']['unit']}", file=sys.stderr, flush=True)
 
     out = {
         "metric": "GEMM TFLOP/s (% MFMA peak) at 4096^3 bf16; int8 GEMV GB/s (% HBM peak)",
@@ -445,7 +533,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (torch.randn on device, seeded)",
+        "data": "synthetic (torch.randn on device, seeded; the CPU leg re-times the same bytes)",
         "config": {"workload": "C2: bf16 NT GEMM M=N=K=4096, fp32 accumulate, bf16 out",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "roofline": head["roofline"] if head else None,
