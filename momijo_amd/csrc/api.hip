@@ -13,6 +13,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 // Scratch of mj_quant_linear_f32_noalloc: the int8 copy of x lives in this
 // file-scope device array instead of a per-call allocation.  Each GPU holds
@@ -54,8 +55,58 @@ int32_t noalloc_scratch(int8_t **out) {
   return MJ_OK;
 }
 
-// Plans and launches an NT GEMM, with a stream-ordered fp32 workspace when the
-// plan splits K.
+// Workspace of the split-K partials: one device buffer per (device, stream),
+// kept by the library and reused by every later call on that stream, so a
+// split-K GEMM makes no allocation call once its stream has seen a call of
+// that size (calls on one stream are ordered, so they never overlap in it).
+// A buffer that has to grow is replaced by one of at least twice its size; the
+// old one is kept until the process ends, since work already queued on the
+// stream may still read it.  A stream under graph capture gets a
+// stream-ordered allocation that belongs to the graph instead.  A stream
+// handle that is destroyed and created again inherits the buffer: a split-K
+// GEMM still running on the destroyed stream must have finished first.
+struct StreamWorkspace {
+  int dev;
+  hipStream_t stream;
+  void *ptr;
+  size_t bytes;
+};
+std::mutex g_ws_mu;
+std::vector<StreamWorkspace> g_ws;
+std::vector<void *> g_ws_retired;
+
+int32_t stream_workspace(size_t bytes, hipStream_t stream, void **out) {
+  int dev = 0;
+  if (int32_t st = hip_status(hipGetDevice(&dev), "hipGetDevice")) return st;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  StreamWorkspace *e = nullptr;
+  for (auto &w : g_ws)
+    if (w.dev == dev && w.stream == stream) e = &w;
+  if (e && e->bytes >= bytes) {
+    *out = e->ptr;
+    return MJ_OK;
+  }
+  size_t want = bytes;
+  if (e && want < 2 * e->bytes) want = 2 * e->bytes;
+  want = (want + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
+  void *p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "split-K workspace allocation of %zu bytes failed", want);
+  }
+  if (e) {
+    g_ws_retired.push_back(e->ptr);
+    e->ptr = p;
+    e->bytes = want;
+  } else {
+    g_ws.push_back({dev, stream, p, want});
+  }
+  *out = p;
+  return MJ_OK;
+}
+
+// Plans and launches an NT GEMM, with the fp32 workspace of the stream when
+// the plan splits K.
 int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
   // The tile kernels address a tile's 256 rows of A and of B with 32-bit
   // buffer offsets ((r * ld + k) * element size, r < 256): larger leading
@@ -66,14 +117,20 @@ int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
                 "(lda=%lld, ldb=%lld)", what, (long long)p.lda, (long long)p.ldb);
   const mj::GemmPlan plan = mj::plan_gemm_nt(p);
   const size_t ws = plan.workspace_bytes(p);
-  if (ws) {
-    if (hipMallocAsync((void **)&p.part, ws, stream) != hipSuccess) {
-      (void)hipGetLastError();
-      return fail(MJ_ERR_ALLOC, "%s: split-K workspace allocation failed", what);
-    }
+  if (!ws) return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (int32_t st = hip_status(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing"))
+    return st;
+  if (cs == hipStreamCaptureStatusNone) {
+    if (int32_t st = stream_workspace(ws, stream, (void **)&p.part)) return st;
+    return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+  }
+  if (hipMallocAsync((void **)&p.part, ws, stream) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "%s: split-K workspace allocation failed", what);
   }
   int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  if (ws) (void)hipFreeAsync(p.part, stream);
+  (void)hipFreeAsync(p.part, stream);
   return st;
 }
 
