@@ -280,16 +280,23 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    # partial last workgroups and waves; other K
                                    # take the 2-rows-per-wave kernel
                                    (1, 37, 1024), (1, 1500, 2048), (1, 4104, 3072),
-                                   (1, 5000, 4096), (1, 7001, 3072), (1, 11008, 4096),
+                                   (1, 7001, 3072),
                                    (1, 16001, 1024), (1, 24000, 2048), (1, 70001, 1024),
+                                   # M = 1, K = 4096: the K-split GEMV at 4, 8,
+                                   # 12, 24, 44 and 64 rows per workgroup with a
+                                   # partial last workgroup, and past 252 * 64
+                                   # rows the streaming GEMV
+                                   (1, 37, 4096), (1, 2000, 4096), (1, 3000, 4096),
+                                   (1, 5000, 4096), (1, 11008, 4096), (1, 16001, 4096),
+                                   (1, 16200, 4096),
                                    (1, 37, 80), (1, 4104, 2064)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
     in any order and under any K split, so the bf16 outputs (after scale,
     bias and rounding) must equal the oracle's bit for bit; this pins every
-    tile, fragment and swizzle index of the 256-row W8A16 kernel and of the
-    skinny-M MFMA GEMV."""
+    tile, fragment and swizzle index of the 256-row W8A16 kernel, of the
+    skinny-M MFMA GEMV and of the M = 1 GEMVs."""
     rng = np.random.default_rng(M + N + K)
     x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
     Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
