@@ -218,7 +218,6 @@ def bench_c3(steps, warmup):
         "weights_rotated_over": copies,
         "cache_hot_GBs": bytes_ / (hot_ms * 1e-3) / 1e9,
         "dispatch_floor_us": floor_ms * 1e3,
-        "streaming_GBs_excluding_floor": bytes_ / ((ms - floor_ms) * 1e-3) / 1e9,
     }
 
 
