@@ -100,6 +100,23 @@ def test_w8a16_split_k_bias_gelu(oracle, dev):
     assert normwise_rel(y, ref) <= BF16_TOL
 
 
+def test_w8a16_split_k_unaligned_scales_bias(oracle, dev):
+    """Scales and bias 4 bytes past a 16-byte boundary: the split-K reduce
+    reads them per element (its 16-byte loads need aligned vectors), with the
+    same result."""
+    x, Q, s, b = _w8(oracle, 64, 1024, 4096, 8)
+    s_store = torch.zeros(1025, dtype=torch.float32, device=dev)
+    b_store = torch.zeros(1025, dtype=torch.float32, device=dev)
+    s_store[1:].copy_(to_dev(s, dev))
+    b_store[1:].copy_(to_dev(b, dev))
+    s_dev, b_dev = s_store[1:], b_store[1:]
+    assert s_dev.data_ptr() % 16 == 4 and b_dev.data_ptr() % 16 == 4
+    lin = mj.W8Linear(to_dev(Q, dev), s_dev, b_dev, mj.EPI_GELU_TANH)
+    y = bf16_host_f32(lin.forward(bf16_dev(x, dev)))
+    _, ref = oracle.linear_w8a16(x, Q, s, b, mj.EPI_GELU_TANH)
+    assert normwise_rel(y, ref) <= BF16_TOL
+
+
 def test_unaligned_operands_are_rejected(dev):
     """The bf16 GEMM needs 16-byte aligned operands and K % 8 == 0: anything
     else is MJ_ERR_UNSUPPORTED, not a fault."""
