@@ -64,7 +64,7 @@ def _args():
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,"
-                   "bwd,f64,copy,vendor); copy and vendor are run only when named")
+                   "qlinear,bwd,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
 
@@ -294,6 +294,34 @@ def bench_c5(steps, warmup):
     }
 
 
+def bench_qlinear(steps, warmup):
+    """QuantLinear.forward (learn/nn/layers.mojo:1681-1685) at 4096^3: the
+    legacy per-tensor W8A8 path -- x quantized with s_x, int8 x int8 -> int32
+    on the int8 matrix cores, dequantize + bias fused, fp32 out.  Not a
+    BASELINE config: it shows the int8 MFMA path against the int8 peak."""
+    import torch
+    import momijo_amd as mj
+    M = N = K = 4096
+    W = _rand_f32((N, K), 11, 0.02)
+    s_w = float(W.abs().max()) / 127.0
+    Wq = torch.clamp(torch.round(W / s_w), -127, 127).to(torch.int8)
+    del W
+    x = mj.Tensor(_rand_f32((M, K), 12))
+    s_x = float(x.torch.abs().max()) / 127.0
+    b = mj.Tensor((torch.rand(N, device="cuda") - 0.5) / 8)
+    ql = mj.QuantLinear(K, N, mj.Tensor(Wq), b, s_w, s_x)
+    ms = _time_launches(lambda i: ql.forward(x), steps, warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    return {
+        "name": "quant_linear_w8a8_4096",
+        "metric": "QuantLinear (per-tensor W8A8) TOP/s, quantize + int8 GEMM + dequant",
+        "value": tops, "unit": "TOP/s", "ms_per_call": ms,
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": tops / PEAK_INT8_TOPS, "traffic": None},
+    }
+
+
 def bench_c1(steps, warmup):
     import torch
     import momijo_amd as mj
@@ -496,7 +524,8 @@ def main():
     print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
-                    ("c5", bench_c5), ("c1", bench_c1), ("bwd", bench_backward),
+                    ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
+                    ("bwd", bench_backward),
                     ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
         if want(key) and (key not in ("copy", "vendor") or key in only):
             rs = fn(a.steps, a.warmup)

@@ -55,10 +55,11 @@ int32_t noalloc_scratch(int8_t **out) {
   return MJ_OK;
 }
 
-// Workspace of the split-K partials: one device buffer per (device, stream),
-// kept by the library and reused by every later call on that stream, so a
-// split-K GEMM makes no allocation call once its stream has seen a call of
-// that size (calls on one stream are ordered, so they never overlap in it).
+// Workspace of the split-K partials and of QuantLinear's int8 copy of x: one
+// device buffer per (device, stream), kept by the library and reused by every
+// later call on that stream, so such a call makes no allocation call once its
+// stream has seen a call of that size (calls on one stream are ordered, so
+// they never overlap in it).
 // A buffer that has to grow is replaced by one of at least twice its size; the
 // old one is kept until the process ends, since work already queued on the
 // stream may still read it.  A stream under graph capture gets a
@@ -105,6 +106,26 @@ int32_t stream_workspace(size_t bytes, hipStream_t stream, void **out) {
   return MJ_OK;
 }
 
+// Workspace of `bytes` for work enqueued on `stream`: the stream's library
+// buffer (stream_workspace), or under graph capture a stream-ordered
+// allocation (*owned = true) to be released by release_workspace.
+int32_t acquire_workspace(size_t bytes, hipStream_t stream, void **out, bool *owned) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (int32_t st = hip_status(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing"))
+    return st;
+  *owned = cs != hipStreamCaptureStatusNone;
+  if (!*owned) return stream_workspace(bytes, stream, out);
+  if (hipMallocAsync(out, bytes, stream) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MJ_ERR_ALLOC, "workspace allocation of %zu bytes failed", bytes);
+  }
+  return MJ_OK;
+}
+
+void release_workspace(void *p, bool owned, hipStream_t stream) {
+  if (owned) (void)hipFreeAsync(p, stream);
+}
+
 // Plans and launches an NT GEMM, with the fp32 workspace of the stream when
 // the plan splits K.
 int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
@@ -118,19 +139,10 @@ int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
   const mj::GemmPlan plan = mj::plan_gemm_nt(p);
   const size_t ws = plan.workspace_bytes(p);
   if (!ws) return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (int32_t st = hip_status(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing"))
-    return st;
-  if (cs == hipStreamCaptureStatusNone) {
-    if (int32_t st = stream_workspace(ws, stream, (void **)&p.part)) return st;
-    return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  }
-  if (hipMallocAsync((void **)&p.part, ws, stream) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "%s: split-K workspace allocation failed", what);
-  }
-  int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  (void)hipFreeAsync(p.part, stream);
+  bool owned = false;
+  if (int32_t st = acquire_workspace(ws, stream, (void **)&p.part, &owned)) return st;
+  const int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+  release_workspace(p.part, owned, stream);
   return st;
 }
 
@@ -520,15 +532,14 @@ int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, fl
   if (int32_t s = check_dims(M, N, K)) return s;
   if (M == 0 || N == 0) return MJ_OK;
   if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
+  // the int8 copy of x in the stream's workspace
   int8_t *xq = nullptr;
-  const size_t bytes = (size_t)M * K + 16;
-  if (hipMallocAsync((void **)&xq, bytes, S(stream)) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
-  }
+  bool owned = false;
+  if (int32_t st = acquire_workspace((size_t)M * K + 16, S(stream), (void **)&xq, &owned))
+    return st;
   const int32_t st = quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq,
                                        S(stream));
-  (void)hipFreeAsync(xq, S(stream));
+  release_workspace(xq, owned, S(stream));
   return st;
 }
 

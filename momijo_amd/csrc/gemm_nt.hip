@@ -869,6 +869,253 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
 }
 
 // ---------------------------------------------------------------------------
+// int8 x int8 -> int32 on 256 x 256 tiles with one wave per SIMD:
+// matmul_i8_i8_to_i32 (learn/api/functional.mojo:249-279) and QuantLinear's
+// dequantize (learn/nn/layers.mojo:1681-1685, functional.mojo:281-302) fused
+// into the epilogue, for problems large enough to fill the CUs with 256 x 256
+// tiles.  It is gemm_nt_w4_kernel's pipeline on int8 data: a 128-deep int8
+// stage is 128 bytes per row, the same LDS bytes as a 64-deep bf16 stage, so
+// the buffers, the XOR swizzle, the direct loads and the fragment reads are
+// byte for byte the same; a lane's 16-byte fragment of a 64-deep step is the
+// 16 consecutive k at 16 (lane / 16) of its row, which is the operand layout
+// of v_mfma_i32_16x16x64_i8 (16 x 16 x 64 per instruction, twice the work of
+// the bf16 16 x 16 x 32 in the same issue slot).  Integer sums are exact, so
+// the result is the reference's in any order.
+//
+// Epilogue (MODE): 0 = the int32 sums C[m, n]; 1 = QuantLinear's
+// y[m, n] = float(acc) * sf + b[n] in fp32 (no FMA contraction).
+struct GemmI8 {
+  const int8_t *A = nullptr;  // [M, K], leading dimension lda
+  int64_t lda = 0;
+  const int8_t *B = nullptr;  // [N, K] (the stored w_q layout), leading dimension ldb
+  int64_t ldb = 0;
+  int32_t *C = nullptr;       // MODE 0: [M, N] int32, leading dimension ldc
+  float *Y = nullptr;         // MODE 1: [M, N] fp32, leading dimension ldc
+  int64_t ldc = 0;
+  float sf = 1.0f;            // MODE 1: s_x * s_w
+  const float *bias = nullptr;  // MODE 1: [N]
+  int64_t M = 0, N = 0, K = 0;
+};
+
+__device__ __forceinline__ void mfma_i8_16x16x64_tied(i32x4 &acc, const bf16x8 &a,
+                                                      const bf16x8 &b) {
+  asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int WM = 128, WN = 128, TM = 8, TN = 8;
+  constexpr int DPO = 8;    // 1-KB direct loads per wave per operand per stage
+  constexpr int KS = 128;   // int8 k per stage (128 bytes per row, as kBK bf16)
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  uint16_t *As = lds;                    // [2][BM][128 B]: stage kt in buffer kt % 2
+  uint16_t *Bs = lds + 2 * BM * kBK;     // [3][BN][128 B]: stage kt in buffer kt % 3
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  int tm, tn;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, 4, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = (K + KS - 1) / KS;
+
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(p.A + (size_t)m0 * p.lda, (int64_t)(M - m0) * p.lda);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(p.B + (size_t)n0 * p.ldb, (int64_t)(N - n0) * p.ldb);
+  // 1-KB block b = i*4 + wave covers tile rows [8b, 8b+8): row 8b + lane/8,
+  // stored chunk lane%8, which holds logical 16-byte chunk c of the row
+  uint32_t a_off[DPO], b_off[DPO];
+  int kc[DPO];
+#pragma unroll
+  for (int i = 0; i < DPO; ++i) {
+    const int r = (i * 4 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    kc[i] = c;
+    a_off[i] = m0 + r < M ? (uint32_t)(r * p.lda + c * 16) : kOobOffset;
+    b_off[i] = n0 + r < N ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
+  }
+  auto load = [&](auto fast, int kt, int buf, int d) {
+    const int k0 = kt * KS;
+    const int i = d & 7;
+    uint16_t *dst = (d < 8 ? As : Bs) + buf * BM * kBK + (i * 4 + wave) * 8 * kBK;
+    const __amdgpu_buffer_rsrc_t r = d < 8 ? rA : rB;
+    const uint32_t off = d < 8 ? a_off[i] : b_off[i];
+    if constexpr (decltype(fast)::value) {
+      dma16s(r, dst, off, (uint32_t)k0);
+    } else {
+      const bool ok = k0 + kc[i] * 16 < K;
+      dma16s(r, dst, ok ? off + k0 : kOobOffset, 0u);
+    }
+  };
+
+  const int fr = lane & 15, fh = lane >> 4;
+  const int sw = (fr >> 1) & 7;
+  const uint16_t *a_rd[2], *b_rd[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int col = ((ks * 4 + fh) ^ sw) * 8;
+    a_rd[ks] = As + (wm * WM + fr) * kBK + col;
+    b_rd[ks] = Bs + (wn * WN + fr) * kBK + col;
+  }
+
+  i32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+  bf16x8 fa[2][TM], fb[2][TN];
+
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int d = 0; d < 2 * DPO; ++d) load(std::false_type(), s, s, d);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DPO) & 0xF) | (((2 * DPO) >> 4) << 14));  // stage 0
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[0][j] = *(const bf16x8 *)(b_rd[0] + j * 16 * kBK);
+  __builtin_amdgcn_s_waitcnt(kLgkm0);
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
+
+  auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
+    constexpr int AB = decltype(ab_c)::value;
+    constexpr int BB = decltype(bb_c)::value;
+    auto read_frag = [&](int t, int dst, int abuf, int bbuf) {
+      if (t < 8) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
+      else fb[dst][t - 8] = *(const bf16x8 *)(b_rd[dst] + bbuf * BN * kBK + (t - 8) * 16 * kBK);
+    };
+    auto group = [&](int j, int src, int dst, int abuf, int bbuf, int load_d, int load_buf) {
+      const int t0 = j < 4 ? 3 * j : 12 + 2 * (j - 4);
+      const int nt = j < 4 ? 3 : (j < 6 ? 2 : 0);
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (u < nt) read_frag(t0 + u, dst, abuf, bbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_i8_16x16x64_tied(acc[u][j], fb[src][j], fa[src][u]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load(fast, kt + 2, load_buf, load_d);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 3; i < TM; ++i) mfma_i8_16x16x64_tied(acc[i][j], fb[src][j], fa[src][i]);
+    };
+#pragma unroll
+    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, 8 + j, (BB + 2) % 3);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | 8);  // vmcnt(8)
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < TN; ++j) group(j, 1, 0, AB ^ 1, (BB + 1) % 3, j, AB);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using F = std::true_type;
+  using S = std::false_type;
+  const int nk_full = K / KS;
+  int kt = 0;
+  for (; kt + 8 <= nk_full; kt += 6) {
+    stage(I0(), I0(), F(), kt);
+    stage(I1(), I1(), F(), kt + 1);
+    stage(I0(), I2(), F(), kt + 2);
+    stage(I1(), I0(), F(), kt + 3);
+    stage(I0(), I1(), F(), kt + 4);
+    stage(I1(), I2(), F(), kt + 5);
+  }
+  for (; kt < nk; kt += 6) {
+    stage(I0(), I0(), S(), kt);
+    if (kt + 1 < nk) stage(I1(), I1(), S(), kt + 1);
+    if (kt + 2 < nk) stage(I0(), I2(), S(), kt + 2);
+    if (kt + 3 < nk) stage(I1(), I0(), S(), kt + 3);
+    if (kt + 4 < nk) stage(I0(), I1(), S(), kt + 4);
+    if (kt + 5 < nk) stage(I1(), I2(), S(), kt + 5);
+  }
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+
+  // a lane's block (i, j) holds output row m0 + wm*WM + 16 i + (lane & 15) at
+  // the 4 columns n0 + wn*WN + 16 j + 4 (lane >> 4) + q
+  const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)(MODE == 0 ? (void *)p.C : (void *)p.Y) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int nb = n0 + wn * WN + j * 16 + 4 * fh;
+    float bq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bq[q] = p.bias ? p.bias[nb + q < N ? nb + q : N - 1] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WM + i * 16 + fr;
+      if (m >= M) continue;
+      if constexpr (MODE == 0) {
+        int32_t *dst = p.C + (size_t)m * p.ldc + nb;
+        if (vec && nb + 3 < N) {
+          *(i32x4 *)dst = acc[i][j];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nb + q < N) dst[q] = acc[i][j][q];
+        }
+      } else {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+          v[q] = (float)acc[i][j][q] * p.sf + bq[q];
+        }
+        float *dst = p.Y + (size_t)m * p.ldc + nb;
+        if (vec && nb + 3 < N) {
+          *(f32x4 *)dst = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nb + q < N) dst[q] = v[q];
+        }
+      }
+    }
+  }
+}
+
+hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
+                             const float *b, int64_t M, int64_t N, int64_t K,
+                             hipStream_t stream) {
+  constexpr size_t lds = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
+  // a tile's 256 rows of K bytes in 32-bit buffer offsets; the scalar K
+  // offset of a stage below 2^31
+  if (256 * K >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 30)) return hipErrorInvalidValue;
+  GemmI8 p;
+  p.A = A; p.lda = K; p.B = B; p.ldb = K; p.C = C; p.Y = y; p.ldc = N;
+  p.sf = sf; p.bias = b; p.M = M; p.N = N; p.K = K;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    for (const void *f : {(const void *)gemm_i8_w4_kernel<0>, (const void *)gemm_i8_w4_kernel<1>}) {
+      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  const int64_t grid = ((M + 255) / 256) * ((N + 255) / 256);
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  if (y)
+    hipLaunchKernelGGL(gemm_i8_w4_kernel<1>, dim3((unsigned)grid), dim3(256), lds, stream, p);
+  else
+    hipLaunchKernelGGL(gemm_i8_w4_kernel<0>, dim3((unsigned)grid), dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // W8A16 tiles with one wave per SIMD: A bf16, B int8 per-channel weights.
 // The same pipeline as gemm_nt_w4_kernel (2 A buffers of 128-byte rows, 3 B
 // buffers, one barrier between the two 32-deep steps of a 64-deep stage, the

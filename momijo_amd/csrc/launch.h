@@ -109,9 +109,18 @@ hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b,
 
 // ---- gemm_i8.hip -----------------------------------------------------------
 // C (int32) = A int8 [M,K] x B^T, B int8 [N,K]; or, with y != null, the fused
-// dequantize y = float(acc)*sf + b.
+// dequantize y = float(acc)*sf + b.  K % 16 == 0 and 16-byte aligned A and B;
+// large problems go to the 256 x 256 kernel below.
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                           const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+// The int8 GEMM on 256 x 256 tiles (gemm_nt.hip), same arguments and
+// conditions as launch_gemm_i8.
+hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
+                             const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+// The 128 x 128 kernel alone (gemm_i8.hip).
+hipError_t launch_gemm_i8_t128(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
+                               const float *b, int64_t M, int64_t N, int64_t K,
+                               hipStream_t stream);
 // Scalar fallback: literal = the reference's stride-ignoring [K,N] read of B,
 // otherwise B [N,K] for shapes/alignments the MFMA kernel does not take.
 hipError_t launch_gemm_i8_scalar(const int8_t *A, const int8_t *B, int32_t *C, float *y,

@@ -129,6 +129,46 @@ def test_int8_gemm_bit_exact(oracle, dev, M, N, K):
     np.testing.assert_array_equal(got, oracle.matmul_i8_i8_to_i32(A, B))
 
 
+def _exact_i8_products(A, B):
+    """A [M,K] . B [N,K]^T of int8 matrices, exactly: every product and
+    partial sum is an integer below 2^53 in magnitude (|acc| <= 2^14 K), so
+    float64 arithmetic is exact in any order."""
+    return (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int64)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 4096),    # 64 tiles of 256 x 256
+                                   (2000, 2100, 4112),    # partial tiles, K % 128 != 0
+                                   (512, 4096, 11008)])   # long K
+def test_int8_gemm_large_tiles_bit_exact(dev, M, N, K):
+    """Shapes that take the 256 x 256 one-wave-per-SIMD int8 kernel: the int32
+    sums must be exact."""
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+    got = mj.matmul_i8_i8_to_i32(mj.Tensor(to_dev(A, dev)),
+                                 mj.Tensor(to_dev(B, dev)).transpose()).numpy()
+    np.testing.assert_array_equal(got.astype(np.int64), _exact_i8_products(A, B))
+
+
+def test_quant_linear_large_bit_exact(oracle, dev):
+    """QuantLinear.forward at 2048 x 2048 x 4096 (the 256 x 256 int8 kernel with
+    the dequantize fused): the oracle's quantize and dequantize around exact
+    int32 sums."""
+    M, N, K = 2048, 2048, 4096
+    x = oracle.randn_f32((M, K), seed=41)
+    W = oracle.randn_f32((N, K), std=0.02, seed=42)
+    b = oracle.randu_f32((N,), -0.0625, 0.0625, seed=43)
+    s_x = oracle.minmax_scale_symmetric(x)
+    s_w = oracle.minmax_scale_symmetric(W)
+    Wq = oracle.quantize_symmetric_int8(W, s_w)
+    xq = oracle.quantize_symmetric_int8(x, s_x)
+    ql = mj.QuantLinear(K, N, mj.Tensor(to_dev(Wq, dev)), mj.Tensor(to_dev(b, dev)), s_w, s_x)
+    got = ql.forward(mj.Tensor(to_dev(x, dev))).numpy()
+    acc = _exact_i8_products(xq, Wq).astype(np.int32)
+    ref = oracle.dequant_i32_bias(acc, np.float32(s_x) * np.float32(s_w), b)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_int8_gemm_legacy_literal(oracle, dev):
     """The reference's stride-ignoring read of w_q.transpose() (bug i):
     result is A @ reshape(w_q.flat, [K, N])."""
