@@ -129,7 +129,8 @@ hipError_t launch_gemm_i8_t128(const int8_t *A, const int8_t *B, int32_t *C, flo
 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                           const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  if (((M + 255) / 256) * ((N + 255) / 256) * K >= kI8W4MinTileK && 256 * K < ((int64_t)1 << 31))
+  if (((M + 255) / 256) * ((N + 255) / 256) * K >= kI8W4MinTileK && 256 * K < ((int64_t)1 << 31) &&
+      K % 16 == 0 && (((uintptr_t)A | (uintptr_t)B) & 15) == 0)
     return launch_gemm_i8_w4(A, B, C, y, sf, b, M, N, K, stream);
   return launch_gemm_i8_t128(A, B, C, y, sf, b, M, N, K, stream);
 }

@@ -1090,8 +1090,11 @@ hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float
                              hipStream_t stream) {
   constexpr size_t lds = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
   // a tile's 256 rows of K bytes in 32-bit buffer offsets; the scalar K
-  // offset of a stage below 2^31
-  if (256 * K >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 30)) return hipErrorInvalidValue;
+  // offset of a stage below 2^31; whole 16-byte chunks of K (a chunk must not
+  // straddle two rows) from 16-byte aligned rows
+  if (256 * K >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 30) || K % 16 != 0 ||
+      (((uintptr_t)A | (uintptr_t)B) & 15) != 0)
+    return hipErrorInvalidValue;
   GemmI8 p;
   p.A = A; p.lda = K; p.B = B; p.ldb = K; p.C = C; p.Y = y; p.ldc = N;
   p.sf = sf; p.bias = b; p.M = M; p.N = N; p.K = K;
