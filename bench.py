@@ -63,7 +63,7 @@ def _args():
     p.add_argument("--settle", type=float, default=0.3,
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c5,"
+    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c4w8a8,c5,"
                    "qlinear,bwd,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
@@ -267,6 +267,30 @@ def bench_c4(steps, warmup):
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
                      "traffic": _traffic("c4_w8a16_prefill_gelu_2048x4096x4096")},
+    }
+
+
+def bench_c4_w8a8(steps, warmup):
+    """C4's shape and epilogue (2048 x 4096 x 4096, bias + GELU, bf16 out) on
+    the W8A8-dynamic path: per-row int8 quantize of x, int8 MFMA with exact
+    int32 sums, both scales + bias + GELU in the epilogue.  The quantize
+    launch is inside the timed region; priced against the int8 peak."""
+    import torch
+    import momijo_amd as mj
+    M, N, K = 2048, 4096, 4096
+    lin = mj.W8A8Linear.from_float(_rand_f32((N, K), 6, 0.02),
+                                   (torch.rand(N, device="cuda") - 0.5) / 8, mj.EPI_GELU_TANH)
+    x = _rand_bf16((M, K), 5)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ms = _time_launches(lambda i: lin.forward(x, out=y), steps, warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    return {
+        "name": "c4_w8a8_dynamic_prefill_gelu_2048x4096x4096",
+        "metric": "W8A8-dynamic Linear + bias + GELU TOP/s (row quantize + int8 GEMM)",
+        "value": tops, "unit": "TOP/s", "ms_per_call": ms,
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": tops / PEAK_INT8_TOPS, "traffic": None},
     }
 
 
@@ -524,7 +548,7 @@ def main():
     print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
-                    ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
+                    ("c4w8a8", bench_c4_w8a8), ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
                     ("bwd", bench_backward),
                     ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
         if want(key) and (key not in ("copy", "vendor") or key in only):

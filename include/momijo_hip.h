@@ -268,6 +268,31 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                         const float *bias, int32_t epilogue, uint16_t *y,
                         int64_t M, int64_t N, int64_t K, void *stream);
 
+/* Dynamic per-row activation quantize: xq[M,K] int8 and sx[M] fp32 from
+ * x[M,K] bf16 by the MJ_ROUND_RHE rule of mj_quantize_rowwise_i8 applied to
+ * each row of x (sx[m] = max|x[m,:]|/127, 1.0 for an all-zero row;
+ * xq = clamp(rne(x/sx[m]), -127, 127); NaN -> 0).  The activation half of
+ * mj_linear_w8a8; the per-tensor reference step it generalises is
+ * quantize_symmetric_int8 with the observer's scale (learn/api/
+ * functional.mojo:231-247, sequential.mojo:232-263). */
+int32_t mj_quantize_rows_bf16_i8(const uint16_t *x, int64_t M, int64_t K, int8_t *xq, float *sx,
+                                 void *stream);
+
+/* W8A8 Linear with dynamic activation scales:
+ *   sx, xq = mj_quantize_rows_bf16_i8(x)
+ *   y[m,n] = bf16(epi(float(xq[m,:] . Q[n,:]) * (sx[m] * scales[n]) + bias[n]))
+ * with the int32 dot product exact on int8 MFMA and the epilogue rounded
+ * step by step in fp32 (sx*scales, then the product, then the bias).  It is
+ * QuantLinear.forward (learn/nn/layers.mojo:1681-1685: quantize x, int8
+ * matmul, dequantize + bias) with per-row scales for x and per-channel scales
+ * for the weights instead of two per-tensor scales.  Same arguments as
+ * mj_linear_w8a16; bias may be NULL; xq and sx live in the stream's
+ * workspace.  Needs K % 16 == 0, K <= 131072 (the int32 sums cannot
+ * overflow) and 16-byte aligned x, Q. */
+int32_t mj_linear_w8a8(const uint16_t *x, const int8_t *Q, const float *scales,
+                       const float *bias, int32_t epilogue, uint16_t *y,
+                       int64_t M, int64_t N, int64_t K, void *stream);
+
 /* Llama-style FFN on W8A16 weights (composition of Linear, silu32 and the
  * elementwise product, tensor/tensor.mojo:4373):
  *   h[M,I] = bf16(silu(x Wg^T * sg) * (x Wu^T * su))   (one fused GEMM; bf16-output silu)
@@ -387,6 +412,10 @@ int32_t mj_quantize_rowwise_i8_h(const float *W, int64_t N, int64_t K, int32_t r
 int32_t mj_linear_w8a16_h(const uint16_t *x, const int8_t *Q, const float *scales,
                           const float *bias, int32_t epilogue, uint16_t *y,
                           int64_t M, int64_t N, int64_t K);
+/* W8A8 Linear with dynamic activation scales (see mj_linear_w8a8). */
+int32_t mj_linear_w8a8_h(const uint16_t *x, const int8_t *Q, const float *scales,
+                         const float *bias, int32_t epilogue, uint16_t *y,
+                         int64_t M, int64_t N, int64_t K);
 /* W8A16 FFN (no reference counterpart; see mj_mlp_w8a16); h may be NULL,
  * then the intermediate stays on the device. */
 int32_t mj_mlp_w8a16_h(const uint16_t *x, const int8_t *Wg, const float *sg,

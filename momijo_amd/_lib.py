@@ -70,6 +70,8 @@ SIGNATURES = {
     "mj_quant_linear_f32_noalloc": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32, _P]),
     "mj_quantize_rowwise_i8": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
     "mj_linear_w8a16": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _P]),
+    "mj_quantize_rows_bf16_i8": (_I32, [_P, _I64, _I64, _P, _P, _P]),
+    "mj_linear_w8a8": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _P]),
     "mj_mlp_w8a16": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     # device memory and streams
     "mj_malloc": (_I32, [ctypes.POINTER(_P), _I64]),
@@ -101,6 +103,7 @@ SIGNATURES = {
     "mj_quant_linear_f32_h": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32]),
     "mj_quantize_rowwise_i8_h": (_I32, [_P, _I64, _I64, _I32, _P, _P]),
     "mj_linear_w8a16_h": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64]),
+    "mj_linear_w8a8_h": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64]),
     "mj_mlp_w8a16_h": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
 }
 

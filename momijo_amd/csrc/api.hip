@@ -55,17 +55,19 @@ int32_t noalloc_scratch(int8_t **out) {
   return MJ_OK;
 }
 
-// Workspace of the split-K partials and of QuantLinear's int8 copy of x: one
-// device buffer per (device, stream), kept by the library and reused by every
-// later call on that stream, so such a call makes no allocation call once its
-// stream has seen a call of that size (calls on one stream are ordered, so
-// they never overlap in it).
+// Workspace of the split-K partials, of QuantLinear's int8 copy of x and of
+// the W8A8 Linear's int8 x and row scales: one device buffer per (device,
+// stream), kept by the library and reused by every later call on that stream,
+// so such a call makes no allocation call once its stream has seen a call of
+// that size (calls on one stream are ordered, so they never overlap in it).
 // A buffer that has to grow is replaced by one of at least twice its size; the
 // old one is kept until the process ends, since work already queued on the
-// stream may still read it.  A stream under graph capture gets a
-// stream-ordered allocation that belongs to the graph instead.  A stream
-// handle that is destroyed and created again inherits the buffer: a split-K
-// GEMM still running on the destroyed stream must have finished first.
+// stream may still read it.  A stream handle that is destroyed and created
+// again inherits the buffer: a split-K GEMM still running on the destroyed
+// stream must have finished first.  These calls are refused under graph
+// capture (MJ_ERR_UNSUPPORTED): a graph replayed on another stream would
+// share the buffer with eager calls; capture-safe callers use the entry
+// points that need no workspace, or mj_quant_linear_f32_noalloc.
 struct StreamWorkspace {
   int dev;
   hipStream_t stream;
@@ -106,24 +108,18 @@ int32_t stream_workspace(size_t bytes, hipStream_t stream, void **out) {
   return MJ_OK;
 }
 
-// Workspace of `bytes` for work enqueued on `stream`: the stream's library
-// buffer (stream_workspace), or under graph capture a stream-ordered
-// allocation (*owned = true) to be released by release_workspace.
-int32_t acquire_workspace(size_t bytes, hipStream_t stream, void **out, bool *owned) {
+// Workspace of `bytes` for work enqueued on `stream` (stream_workspace);
+// MJ_ERR_UNSUPPORTED while the stream is being captured into a graph.
+int32_t acquire_workspace(size_t bytes, hipStream_t stream, void **out) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (int32_t st = hip_status(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing"))
     return st;
-  *owned = cs != hipStreamCaptureStatusNone;
-  if (!*owned) return stream_workspace(bytes, stream, out);
-  if (hipMallocAsync(out, bytes, stream) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "workspace allocation of %zu bytes failed", bytes);
-  }
-  return MJ_OK;
-}
-
-void release_workspace(void *p, bool owned, hipStream_t stream) {
-  if (owned) (void)hipFreeAsync(p, stream);
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(MJ_ERR_UNSUPPORTED,
+                "this call needs the library's per-stream workspace, which is not available "
+                "under graph capture (mj_quant_linear_f32_noalloc, the GEMV (M <= 16) and "
+                "the GEMMs without a K split can be captured)");
+  return stream_workspace(bytes, stream, out);
 }
 
 // Plans and launches an NT GEMM, with the fp32 workspace of the stream when
@@ -139,11 +135,8 @@ int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
   const mj::GemmPlan plan = mj::plan_gemm_nt(p);
   const size_t ws = plan.workspace_bytes(p);
   if (!ws) return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  bool owned = false;
-  if (int32_t st = acquire_workspace(ws, stream, (void **)&p.part, &owned)) return st;
-  const int32_t st = hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  release_workspace(p.part, owned, stream);
-  return st;
+  if (int32_t st = acquire_workspace(ws, stream, (void **)&p.part)) return st;
+  return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
 }
 
 // QuantLinear.forward on a caller-provided int8 buffer xq of M*K bytes
@@ -534,13 +527,8 @@ int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, fl
   if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
   // the int8 copy of x in the stream's workspace
   int8_t *xq = nullptr;
-  bool owned = false;
-  if (int32_t st = acquire_workspace((size_t)M * K + 16, S(stream), (void **)&xq, &owned))
-    return st;
-  const int32_t st = quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq,
-                                       S(stream));
-  release_workspace(xq, owned, S(stream));
-  return st;
+  if (int32_t st = acquire_workspace((size_t)M * K + 16, S(stream), (void **)&xq)) return st;
+  return quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq, S(stream));
 }
 
 int32_t mj_quant_linear_f32_noalloc(const float *x, const int8_t *Wq, const float *b, float s_w,
@@ -588,6 +576,45 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
   p.A = x; p.lda = K; p.B = Q; p.ldb = K; p.scales = scales; p.bias = bias; p.epi = epilogue;
   p.C = y; p.ldc = N; p.M = M; p.N = N; p.K = K; p.bkind = mj::B_INT8;
   return run_gemm_nt(p, S(stream), "gemm_w8a16");
+}
+
+int32_t mj_quantize_rows_bf16_i8(const uint16_t *x, int64_t M, int64_t K, int8_t *xq, float *sx,
+                                 void *stream) {
+  if (int32_t s = check_dims(M, 0, K)) return s;
+  if (M == 0) return MJ_OK;
+  if (K == 0) return fail(MJ_ERR_SHAPE, "K must be positive");
+  if (!x || !xq || !sx) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_quantize_rows_bf16(x, M, K, xq, sx, S(stream)),
+                    "quantize_rows_bf16 launch");
+}
+
+int32_t mj_linear_w8a8(const uint16_t *x, const int8_t *Q, const float *scales, const float *bias,
+                       int32_t epilogue, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                       void *stream) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0) return MJ_OK;
+  if (K == 0) return fail(MJ_ERR_SHAPE, "K must be positive");
+  if (!x || !Q || !scales || !y) return fail(MJ_ERR_ARG, "null operand");
+  // K <= 2^17: |sum| <= 127 * 127 * K stays below 2^31, so the int32 sums
+  // are exact
+  if (K % 16 || K > ((int64_t)1 << 17) || !aligned16(x) || !aligned16(Q))
+    return fail(MJ_ERR_UNSUPPORTED,
+                "W8A8 Linear needs K %% 16 == 0, K <= 131072 and 16-byte aligned x, Q");
+  // xq [M,K] int8 then sx [M] fp32 in the stream's workspace
+  const size_t xq_bytes = ((size_t)M * K + 255) & ~(size_t)255;
+  int8_t *ws = nullptr;
+  if (int32_t st = acquire_workspace(xq_bytes + (size_t)M * sizeof(float), S(stream),
+                                     (void **)&ws))
+    return st;
+  float *sx = (float *)(ws + xq_bytes);
+  int32_t st = hip_status(mj::launch_quantize_rows_bf16(x, M, K, ws, sx, S(stream)),
+                          "quantize_rows_bf16 launch");
+  if (st == MJ_OK)
+    st = hip_status(mj::launch_linear_w8a8(ws, sx, Q, scales, bias, epilogue, y, M, N, K,
+                                           S(stream)),
+                    "gemm_w8a8 launch");
+  return st;
 }
 
 int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const int8_t *Wu,

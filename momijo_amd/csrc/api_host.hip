@@ -423,6 +423,22 @@ int32_t mj_linear_w8a16_h(const uint16_t *x, const int8_t *Q, const float *scale
   });
 }
 
+int32_t mj_linear_w8a8_h(const uint16_t *x, const int8_t *Q, const float *scales,
+                         const float *bias, int32_t epilogue, uint16_t *y, int64_t M, int64_t N,
+                         int64_t K) {
+  if (int32_t s = check_dims(M, N, K)) return s;
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!y || !scales || !x || !Q) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[5] = {{x, nullptr, (size_t)(M * K) * 2}, {Q, nullptr, (size_t)(N * K)},
+                  {scales, nullptr, (size_t)N * F4}, {bias, nullptr, opt_bytes(bias, (size_t)N * F4)},
+                  {nullptr, y, (size_t)(M * N) * 2}};
+  return with_device_copies(a, 5, [&](void **d) {
+    return mj_linear_w8a8((const uint16_t *)d[0], (const int8_t *)d[1], (const float *)d[2],
+                          (const float *)d[3], epilogue, (uint16_t *)d[4], M, N, K, nullptr);
+  });
+}
+
 int32_t mj_mlp_w8a16_h(const uint16_t *x, const int8_t *Wg, const float *sg, const int8_t *Wu,
                        const float *su, const int8_t *Wd, const float *sd, uint16_t *h,
                        uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H) {

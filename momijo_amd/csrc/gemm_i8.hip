@@ -7,8 +7,15 @@
 //
 // 128x128 tile per 256-thread workgroup, 64-wide K stages of int8 in LDS
 // (rows padded to 80 B so 16-byte fragment reads of 16 lanes hit distinct
-// banks), double-buffered through registers; problems large enough for
-// 256 x 256 tiles go to gemm_i8_w4_kernel (gemm_nt.hip).
+// banks), double-buffered through registers.  It only runs where the
+// one-wave-per-SIMD kernel (gemm_i8_w4_kernel in gemm_nt.hip, 256 x 256 or
+// 256 x 128 tiles) cannot address a tile with 32-bit offsets (256 K >= 2^31):
+// that kernel is faster at every measured shape.  MI355X, bit-identical
+// outputs, this kernel against it: 4096^3 128.9 / 62.5 us, 3072 x 4096 x 4096
+// 93.3 / 57.4, 2048 x 4096 x 4096 66.3 / 36.8, 1024 x 4096 x 4096 50.1 / 30.7,
+// 512 x 11008 x 4096 58.5 / 33.6, 512 x 4096 x 11008 110.2 / 64.9, 1024 x
+// 1024 x 4096 40.6 / 28.3, 1000 x 3000 x 1040 21.2 / 16.8, 300 x 520 x 4112
+// 39.5 / 25.2, 512 x 512 x 4096 39.2 / 24.7.
 #include "common.h"
 #include "launch.h"
 
@@ -16,14 +23,6 @@ namespace mj {
 
 constexpr int kIBM = 128, kIBN = 128, kIBK = 64;
 constexpr int kILds = kIBK + 16;  // bytes per LDS row
-// Problems whose 256 x 256 tiles times K reach 64 * 4096 take the
-// one-wave-per-SIMD kernel (gemm_i8_w4_kernel in gemm_nt.hip).  Measured on
-// MI355X against this file's 128 x 128 kernel (bit-identical outputs):
-// 4096^3 62.0 against 129.1 us, 2048 x 4096 x 4096 54.2 / 67.7, 512 x 11008 x
-// 4096 51.3 / 58.0, 512 x 4096 x 11008 (32 tiles) 97.3 / 110.2, 1024 x 4096 x
-// 4096 (64 tiles) even; 1000 x 3000 x 1040 (48 tiles) 27.7 / 21.1 and
-// 300 x 520 x 4112 46.4 / 39.7 favour the small tiles.
-constexpr int64_t kI8W4MinTileK = (int64_t)64 * 4096;
 
 __global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t *__restrict__ A,
                                                       const int8_t *__restrict__ B,
@@ -129,8 +128,7 @@ hipError_t launch_gemm_i8_t128(const int8_t *A, const int8_t *B, int32_t *C, flo
 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                           const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  if (((M + 255) / 256) * ((N + 255) / 256) * K >= kI8W4MinTileK && 256 * K < ((int64_t)1 << 31) &&
-      K % 16 == 0 && (((uintptr_t)A | (uintptr_t)B) & 15) == 0)
+  if (256 * K < ((int64_t)1 << 31) && K % 16 == 0 && (((uintptr_t)A | (uintptr_t)B) & 15) == 0)
     return launch_gemm_i8_w4(A, B, C, y, sf, b, M, N, K, stream);
   return launch_gemm_i8_t128(A, B, C, y, sf, b, M, N, K, stream);
 }

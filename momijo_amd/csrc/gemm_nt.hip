@@ -869,21 +869,26 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
 }
 
 // ---------------------------------------------------------------------------
-// int8 x int8 -> int32 on 256 x 256 tiles with one wave per SIMD:
-// matmul_i8_i8_to_i32 (learn/api/functional.mojo:249-279) and QuantLinear's
+// int8 x int8 -> int32 on 256 x BN tiles (BN = 256 or 128) with one wave per
+// SIMD: matmul_i8_i8_to_i32 (learn/api/functional.mojo:249-279), QuantLinear's
 // dequantize (learn/nn/layers.mojo:1681-1685, functional.mojo:281-302) fused
-// into the epilogue, for problems large enough to fill the CUs with 256 x 256
-// tiles.  It is gemm_nt_w4_kernel's pipeline on int8 data: a 128-deep int8
-// stage is 128 bytes per row, the same LDS bytes as a 64-deep bf16 stage, so
-// the buffers, the XOR swizzle, the direct loads and the fragment reads are
-// byte for byte the same; a lane's 16-byte fragment of a 64-deep step is the
-// 16 consecutive k at 16 (lane / 16) of its row, which is the operand layout
-// of v_mfma_i32_16x16x64_i8 (16 x 16 x 64 per instruction, twice the work of
-// the bf16 16 x 16 x 32 in the same issue slot).  Integer sums are exact, so
-// the result is the reference's in any order.
+// into the epilogue, and the W8A8 Linear with per-row activation and
+// per-channel weight scales, for problems large enough to fill the CUs.  It is
+// gemm_nt_w4_kernel's pipeline on int8 data: a 128-deep int8 stage is 128
+// bytes per row, the same LDS bytes as a 64-deep bf16 stage, so the buffers,
+// the XOR swizzle, the direct loads and the fragment reads are byte for byte
+// the same; a lane's 16-byte fragment of a 64-deep step is the 16 consecutive
+// k at 16 (lane / 16) of its row, which is the operand layout of
+// v_mfma_i32_16x16x64_i8 (16 x 16 x 64 per instruction, twice the work of the
+// bf16 16 x 16 x 32 in the same issue slot).  Integer sums are exact, so the
+// sums are the reference's in any order.  BN = 128 (waves of 128 x 64) gives
+// twice the workgroups where 256 x 256 tiles would leave CUs idle; its step 1
+// issues two A loads per MFMA group instead of one.
 //
 // Epilogue (MODE): 0 = the int32 sums C[m, n]; 1 = QuantLinear's
-// y[m, n] = float(acc) * sf + b[n] in fp32 (no FMA contraction).
+// y[m, n] = float(acc) * sf + b[n] in fp32; 2 = the W8A8 Linear's
+// y[m, n] = bf16(epi(float(acc) * (sx[m] * sw[n]) + b[n])) (no FMA contraction
+// in either; epi as the bf16-output epilogues of the W8A16 kernels).
 struct GemmI8 {
   const int8_t *A = nullptr;  // [M, K], leading dimension lda
   int64_t lda = 0;
@@ -891,9 +896,13 @@ struct GemmI8 {
   int64_t ldb = 0;
   int32_t *C = nullptr;       // MODE 0: [M, N] int32, leading dimension ldc
   float *Y = nullptr;         // MODE 1: [M, N] fp32, leading dimension ldc
+  uint16_t *Yb = nullptr;     // MODE 2: [M, N] bf16, leading dimension ldc
   int64_t ldc = 0;
   float sf = 1.0f;            // MODE 1: s_x * s_w
-  const float *bias = nullptr;  // MODE 1: [N]
+  const float *sx = nullptr;  // MODE 2: per-row activation scales [M]
+  const float *sw = nullptr;  // MODE 2: per-channel weight scales [N]
+  const float *bias = nullptr;  // MODES 1, 2: [N] (may be null in MODE 2)
+  int epi = 0;                // MODE 2
   int64_t M = 0, N = 0, K = 0;
 };
 
@@ -902,12 +911,67 @@ __device__ __forceinline__ void mfma_i8_16x16x64_tied(i32x4 &acc, const bf16x8 &
   asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-template <int MODE>
+// MODE 2 epilogue for activation E: a lane's block (i, j) holds output row
+// m0 + wm*128 + 16 i + (lane & 15) at the 4 columns nb_j .. nb_j + 3.
+template <int E, int TM, int TN, int WN>
+__device__ __forceinline__ void store_w8a8(const GemmI8 &p, const i32x4 (&acc)[TM][TN], int m0,
+                                           int n0, int wm, int wn, int lane) {
+  const int M = (int)p.M, N = (int)p.N;
+  const int fr = lane & 15, fh = lane >> 4;
+  const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.Yb & 7) == 0;
+  float sxm[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * 128 + i * 16 + fr;
+    sxm[i] = p.sx[m < M ? m : M - 1];
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int nb = n0 + wn * WN + j * 16 + 4 * fh;
+    float swq[4], bq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + q < N ? nb + q : N - 1;
+      swq[q] = p.sw[n];
+      bq[q] = p.bias ? p.bias[n] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * 128 + i * 16 + fr;
+      if (m >= M) continue;
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t;
+        {
+#pragma clang fp contract(off)
+          const float sf = sxm[i] * swq[q];
+          t = (float)acc[i][j][q] * sf;
+          if (p.bias) t = t + bq[q];
+        }
+        v[q] = apply_epi_b16(E, t);
+      }
+      uint16_t *dst = p.Yb + (size_t)m * p.ldc + nb;
+      if (vec && nb + 3 < N) {
+        *(uint2 *)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < N) dst[q] = (uint16_t)f32_to_bf16_bits(v[q]);
+      }
+    }
+  }
+}
+
+template <int BN, int MODE>
 __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
-  constexpr int BM = 256, BN = 256;
-  constexpr int WM = 128, WN = 128, TM = 8, TN = 8;
-  constexpr int DPO = 8;    // 1-KB direct loads per wave per operand per stage
-  constexpr int KS = 128;   // int8 k per stage (128 bytes per row, as kBK bf16)
+  constexpr int BM = 256;
+  constexpr int WM = 128, WN = BN / 2, TM = 8, TN = WN / 16;
+  constexpr int DPA = 8;       // 1-KB direct loads of A per wave per stage
+  constexpr int DPB = BN / 32;  // of B
+  constexpr int A_PER_GROUP = DPA / TN;  // A loads per MFMA group of step 1
+  constexpr int KS = 128;      // int8 k per stage (128 bytes per row, as kBK bf16)
+  static_assert(BN == 128 || BN == 256, "tile width");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t *As = lds;                    // [2][BM][128 B]: stage kt in buffer kt % 2
   uint16_t *Bs = lds + 2 * BM * kBK;     // [3][BN][128 B]: stage kt in buffer kt % 3
@@ -926,20 +990,23 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(p.B + (size_t)n0 * p.ldb, (int64_t)(N - n0) * p.ldb);
   // 1-KB block b = i*4 + wave covers tile rows [8b, 8b+8): row 8b + lane/8,
   // stored chunk lane%8, which holds logical 16-byte chunk c of the row
-  uint32_t a_off[DPO], b_off[DPO];
-  int kc[DPO];
+  uint32_t a_off[DPA], b_off[DPB];
+  int kc[DPA];
 #pragma unroll
-  for (int i = 0; i < DPO; ++i) {
+  for (int i = 0; i < DPA; ++i) {
     const int r = (i * 4 + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     kc[i] = c;
     a_off[i] = m0 + r < M ? (uint32_t)(r * p.lda + c * 16) : kOobOffset;
-    b_off[i] = n0 + r < N ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
+    if (i < DPB) b_off[i] = n0 + r < N ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
   }
+  // direct load d of stage kt into buffer buf: d < 8 is A block d, else B
+  // block d - 8 (< DPB)
   auto load = [&](auto fast, int kt, int buf, int d) {
     const int k0 = kt * KS;
     const int i = d & 7;
-    uint16_t *dst = (d < 8 ? As : Bs) + buf * BM * kBK + (i * 4 + wave) * 8 * kBK;
+    uint16_t *dst = d < 8 ? As + buf * BM * kBK + (i * 4 + wave) * 8 * kBK
+                          : Bs + buf * BN * kBK + (i * 4 + wave) * 8 * kBK;
     const __amdgpu_buffer_rsrc_t r = d < 8 ? rA : rB;
     const uint32_t off = d < 8 ? a_off[i] : b_off[i];
     if constexpr (decltype(fast)::value) {
@@ -968,10 +1035,14 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   bf16x8 fa[2][TM], fb[2][TN];
 
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < 2; ++s) {
 #pragma unroll
-    for (int d = 0; d < 2 * DPO; ++d) load(std::false_type(), s, s, d);
-  __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DPO) & 0xF) | (((2 * DPO) >> 4) << 14));  // stage 0
+    for (int d = 0; d < DPA; ++d) load(std::false_type(), s, s, d);
+#pragma unroll
+    for (int d = 0; d < DPB; ++d) load(std::false_type(), s, s, 8 + d);
+  }
+  constexpr int kStage = DPA + DPB;  // loads per stage: wait for stage 0
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (kStage & 0xF) | ((kStage >> 4) << 14));
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
   for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
@@ -983,11 +1054,16 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
     constexpr int AB = decltype(ab_c)::value;
     constexpr int BB = decltype(bb_c)::value;
+    // read t < 8: A block t, else B block t - 8
     auto read_frag = [&](int t, int dst, int abuf, int bbuf) {
       if (t < 8) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
       else fb[dst][t - 8] = *(const bf16x8 *)(b_rd[dst] + bbuf * BN * kBK + (t - 8) * 16 * kBK);
     };
-    auto group = [&](int j, int src, int dst, int abuf, int bbuf, int load_d, int load_buf) {
+    // the 8 + TN fragment reads of a step go 3 per group into groups 0-3,
+    // then (TN = 8) 2, 2 into groups 4-5; a group's loads go after its third
+    // MFMA and (a second one) after its sixth
+    auto group = [&](int j, int src, int dst, int abuf, int bbuf, int load_d, int nld,
+                     int load_buf) {
       const int t0 = j < 4 ? 3 * j : 12 + 2 * (j - 4);
       const int nt = j < 4 ? 3 : (j < 6 ? 2 : 0);
 #pragma unroll
@@ -1001,16 +1077,26 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
       load(fast, kt + 2, load_buf, load_d);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 3; i < TM; ++i) mfma_i8_16x16x64_tied(acc[i][j], fb[src][j], fa[src][i]);
+      for (int i = 3; i < TM; ++i) {
+        mfma_i8_16x16x64_tied(acc[i][j], fb[src][j], fa[src][i]);
+        if (i == 5 && nld > 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          load(fast, kt + 2, load_buf, load_d + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
     };
+    // step 0; B loads of stage kt+2 into B buffer (BB + 2) % 3
 #pragma unroll
-    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, 8 + j, (BB + 2) % 3);
+    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, 8 + j, 1, (BB + 2) % 3);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | 8);  // vmcnt(8)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | DPB);  // vmcnt(DPB): all but this step's B loads
     asm volatile("s_barrier" ::: "memory");
+    // step 1; A loads of stage kt+2 into A buffer AB
 #pragma unroll
-    for (int j = 0; j < TN; ++j) group(j, 1, 0, AB ^ 1, (BB + 1) % 3, j, AB);
+    for (int j = 0; j < TN; ++j)
+      group(j, 1, 0, AB ^ 1, (BB + 1) % 3, A_PER_GROUP * j, A_PER_GROUP, AB);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
   };
@@ -1041,6 +1127,20 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
+  if constexpr (MODE == 2) {
+    switch (p.epi) {
+#define MJ_W8A8(E) store_w8a8<E, TM, TN, WN>(p, acc, m0, n0, wm, wn, lane); break;
+      case EPI_RELU: MJ_W8A8(EPI_RELU)
+      case EPI_GELU_TANH: MJ_W8A8(EPI_GELU_TANH)
+      case EPI_SILU: MJ_W8A8(EPI_SILU)
+      case EPI_GELU_TANH_APPROX: MJ_W8A8(EPI_GELU_TANH_APPROX)
+      case EPI_SILU_APPROX: MJ_W8A8(EPI_SILU_APPROX)
+      case EPI_RELU_UNARY: MJ_W8A8(EPI_RELU_UNARY)
+      default: MJ_W8A8(EPI_NONE)
+#undef MJ_W8A8
+    }
+    return;
+  }
   // a lane's block (i, j) holds output row m0 + wm*WM + 16 i + (lane & 15) at
   // the 4 columns n0 + wn*WN + 16 j + 4 (lane >> 4) + q
   const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)(MODE == 0 ? (void *)p.C : (void *)p.Y) & 15) == 0;
@@ -1085,37 +1185,60 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   }
 }
 
-hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
-                             const float *b, int64_t M, int64_t N, int64_t K,
-                             hipStream_t stream) {
-  constexpr size_t lds = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
+// Launches gemm_i8_w4_kernel<BN, MODE> for p: 256 x 256 tiles when they
+// cover at least 192 CUs' worth of workgroups, else 256 x 128.
+template <int MODE>
+static hipError_t launch_i8_w4(const GemmI8 &p, hipStream_t stream) {
+  constexpr size_t lds256 = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
+  constexpr size_t lds128 = size_t(2 * 256 + 3 * 128) * kBK * sizeof(uint16_t);  // 112 KB
   // a tile's 256 rows of K bytes in 32-bit buffer offsets; the scalar K
   // offset of a stage below 2^31; whole 16-byte chunks of K (a chunk must not
   // straddle two rows) from 16-byte aligned rows
-  if (256 * K >= ((int64_t)1 << 31) || K >= ((int64_t)1 << 30) || K % 16 != 0 ||
-      (((uintptr_t)A | (uintptr_t)B) & 15) != 0)
+  if (256 * p.lda >= ((int64_t)1 << 31) || 256 * p.ldb >= ((int64_t)1 << 31) ||
+      p.K >= ((int64_t)1 << 30) || p.K % 16 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 ||
+      (((uintptr_t)p.A | (uintptr_t)p.B) & 15) != 0)
     return hipErrorInvalidValue;
-  GemmI8 p;
-  p.A = A; p.lda = K; p.B = B; p.ldb = K; p.C = C; p.Y = y; p.ldc = N;
-  p.sf = sf; p.bias = b; p.M = M; p.N = N; p.K = K;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
   const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
   if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
-    for (const void *f : {(const void *)gemm_i8_w4_kernel<0>, (const void *)gemm_i8_w4_kernel<1>}) {
-      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
+    hipError_t e = hipFuncSetAttribute((const void *)gemm_i8_w4_kernel<256, MODE>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds256);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)gemm_i8_w4_kernel<128, MODE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds128);
+    if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  const int64_t grid = ((M + 255) / 256) * ((N + 255) / 256);
-  if (grid > INT32_MAX) return hipErrorInvalidValue;
-  if (y)
-    hipLaunchKernelGGL(gemm_i8_w4_kernel<1>, dim3((unsigned)grid), dim3(256), lds, stream, p);
+  const int64_t tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const int64_t tiles128 = ((p.M + 255) / 256) * ((p.N + 127) / 128);
+  if (tiles128 > INT32_MAX) return hipErrorInvalidValue;
+  if (tiles256 >= 192)
+    hipLaunchKernelGGL((gemm_i8_w4_kernel<256, MODE>), dim3((unsigned)tiles256), dim3(256), lds256,
+                       stream, p);
   else
-    hipLaunchKernelGGL(gemm_i8_w4_kernel<0>, dim3((unsigned)grid), dim3(256), lds, stream, p);
+    hipLaunchKernelGGL((gemm_i8_w4_kernel<128, MODE>), dim3((unsigned)tiles128), dim3(256), lds128,
+                       stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
+                             const float *b, int64_t M, int64_t N, int64_t K,
+                             hipStream_t stream) {
+  GemmI8 p;
+  p.A = A; p.lda = K; p.B = B; p.ldb = K; p.C = C; p.Y = y; p.ldc = N;
+  p.sf = sf; p.bias = b; p.M = M; p.N = N; p.K = K;
+  return y ? launch_i8_w4<1>(p, stream) : launch_i8_w4<0>(p, stream);
+}
+
+hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *Wq,
+                              const float *sw, const float *bias, int epi, uint16_t *y,
+                              int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  GemmI8 p;
+  p.A = xq; p.lda = K; p.B = Wq; p.ldb = K; p.Yb = y; p.ldc = N;
+  p.sx = sx; p.sw = sw; p.bias = bias; p.epi = epi; p.M = M; p.N = N; p.K = K;
+  return launch_i8_w4<2>(p, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -106,6 +106,10 @@ hipError_t launch_minmax_scale(const float *x, int64_t n, float max_q, float *pa
                                float *scale_out, hipStream_t stream);
 hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b, float *y,
                                    int64_t M, int64_t N, hipStream_t stream);
+// x [M,K] bf16 -> xq [M,K] int8, sx [M] fp32: per-row RHE quantize (the W8A8
+// Linear's dynamic activation scales).
+hipError_t launch_quantize_rows_bf16(const uint16_t *x, int64_t M, int64_t K, int8_t *xq,
+                                     float *sx, hipStream_t stream);
 
 // ---- gemm_i8.hip -----------------------------------------------------------
 // C (int32) = A int8 [M,K] x B^T, B int8 [N,K]; or, with y != null, the fused
@@ -113,10 +117,16 @@ hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b,
 // large problems go to the 256 x 256 kernel below.
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                           const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream);
-// The int8 GEMM on 256 x 256 tiles (gemm_nt.hip), same arguments and
-// conditions as launch_gemm_i8.
+// The int8 GEMM on 256 x 256 (or, below 192 such tiles, 256 x 128) tiles
+// (gemm_nt.hip), same arguments and conditions as launch_gemm_i8.
 hipError_t launch_gemm_i8_w4(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                              const float *b, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+// The W8A8 Linear's GEMM on the same kernel: y [M,N] bf16 =
+// bf16(epi(float(xq Wq^T) * (sx[m] * sw[n]) + bias[n])); bias may be null.
+// K % 16 == 0, 16-byte aligned xq and Wq.
+hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *Wq,
+                              const float *sw, const float *bias, int epi, uint16_t *y,
+                              int64_t M, int64_t N, int64_t K, hipStream_t stream);
 // The 128 x 128 kernel alone (gemm_i8.hip).
 hipError_t launch_gemm_i8_t128(const int8_t *A, const int8_t *B, int32_t *C, float *y, float sf,
                                const float *b, int64_t M, int64_t N, int64_t K,

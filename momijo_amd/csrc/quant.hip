@@ -151,6 +151,93 @@ hipError_t launch_quantize_rowwise(const float *W, int64_t N, int64_t K, int rou
   return hipGetLastError();
 }
 
+// Dynamic per-row activation quantize for the W8A8 Linear: x [M, K] bf16 ->
+// xq [M, K] int8 and sx [M] fp32 with the RHE rule of quantize_rowwise
+// (scale = max|row| / 127, 1.0 for an all-zero row; q = clamp(rne(x / scale),
+// -127, 127); bf16 -> fp32 is exact).  One wave per row; for K = 512 CH
+// (CH <= 16) the row is held in registers (8 bf16 per 16-byte load), so x and
+// xq are each touched once.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+__device__ __forceinline__ float amax8(uint4 v) {
+  const float a = fmaxf(fmaxf(fabsf(bf16_lo(v.x)), fabsf(bf16_hi(v.x))),
+                        fmaxf(fabsf(bf16_lo(v.y)), fabsf(bf16_hi(v.y))));
+  const float b = fmaxf(fmaxf(fabsf(bf16_lo(v.z)), fabsf(bf16_hi(v.z))),
+                        fmaxf(fabsf(bf16_lo(v.w)), fabsf(bf16_hi(v.w))));
+  return fmaxf(a, b);
+}
+
+__device__ __forceinline__ uint32_t quant_pair2(uint32_t w0, uint32_t w1, float s) {
+  return (uint32_t)(quant_rhe(bf16_lo(w0), s) & 0xFF) |
+         ((uint32_t)(quant_rhe(bf16_hi(w0), s) & 0xFF) << 8) |
+         ((uint32_t)(quant_rhe(bf16_lo(w1), s) & 0xFF) << 16) |
+         ((uint32_t)(quant_rhe(bf16_hi(w1), s) & 0xFF) << 24);
+}
+
+template <int CH>
+__global__ __launch_bounds__(256) void quantize_rows_bf16_reg(const uint16_t *__restrict__ x,
+                                                              int M, int K,
+                                                              int8_t *__restrict__ xq,
+                                                              float *__restrict__ sx) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const uint4 *x4 = (const uint4 *)(x + (size_t)row * K);
+  uint4 v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) v[c] = load_nt16(x4 + c * 64 + lane);
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) amax = fmaxf(amax, amax8(v[c]));
+  amax = wave_max(amax);
+  const float s = row_scale(ROUND_RHE, amax, 0.0f, 0.0f);
+  uint2 *q2 = (uint2 *)(xq + (size_t)row * K);
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+    q2[c * 64 + lane] = make_uint2(quant_pair2(v[c].x, v[c].y, s), quant_pair2(v[c].z, v[c].w, s));
+  if (lane == 0) sx[row] = s;
+}
+
+__global__ __launch_bounds__(256) void quantize_rows_bf16_any(const uint16_t *__restrict__ x,
+                                                              int M, int K,
+                                                              int8_t *__restrict__ xq,
+                                                              float *__restrict__ sx) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const uint16_t *r = x + (size_t)row * K;
+  float amax = 0.0f;
+  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(bf16_lo(r[k])));
+  amax = wave_max(amax);
+  const float s = row_scale(ROUND_RHE, amax, 0.0f, 0.0f);
+  for (int k = lane; k < K; k += 64) xq[(size_t)row * K + k] = (int8_t)quant_rhe(bf16_lo(r[k]), s);
+  if (lane == 0) sx[row] = s;
+}
+
+hipError_t launch_quantize_rows_bf16(const uint16_t *x, int64_t M, int64_t K, int8_t *xq,
+                                     float *sx, hipStream_t stream) {
+  const unsigned blocks = (unsigned)((M + 3) / 4);
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)xq % 8 == 0);
+  if (aligned && K % 512 == 0 && K <= 8192) {
+    switch (K / 512) {
+#define MJ_QR_CASE(ch)                                                                       \
+  case ch:                                                                                   \
+    hipLaunchKernelGGL(quantize_rows_bf16_reg<ch>, dim3(blocks), dim3(256), 0, stream, x,      \
+                       (int)M, (int)K, xq, sx);                                                \
+    return hipGetLastError();
+      MJ_QR_CASE(1) MJ_QR_CASE(2) MJ_QR_CASE(3) MJ_QR_CASE(4) MJ_QR_CASE(5) MJ_QR_CASE(6)
+      MJ_QR_CASE(7) MJ_QR_CASE(8) MJ_QR_CASE(9) MJ_QR_CASE(10) MJ_QR_CASE(11) MJ_QR_CASE(12)
+      MJ_QR_CASE(13) MJ_QR_CASE(14) MJ_QR_CASE(15) MJ_QR_CASE(16)
+#undef MJ_QR_CASE
+      default: break;
+    }
+  }
+  hipLaunchKernelGGL(quantize_rows_bf16_any, dim3(blocks), dim3(256), 0, stream, x, (int)M,
+                     (int)K, xq, sx);
+  return hipGetLastError();
+}
+
 // quantize_symmetric_int8 (functional.mojo:231-247), per-tensor scale.
 __global__ __launch_bounds__(256) void quantize_tensor_legacy(const float *__restrict__ x, int64_t n,
                                                               float scale,

@@ -182,6 +182,26 @@ class W8Linear:
         return out
 
 
+class W8A8Linear(W8Linear):
+    """W8Linear's weights with the activations quantized too: each row of x
+    gets its own int8 scale (max|row| / 127, round half to even) at call
+    time, the product runs on int8 MFMA with exact int32 sums, and the
+    epilogue applies both scales:
+    y = bf16(epi(float(xq . q^T) * (sx[m] * scale[n]) + bias[n])).
+    The per-row / per-channel form of QuantLinear.forward
+    (learn/nn/layers.mojo:1681-1685).  For prefill-sized M; decode (M = 1)
+    is faster on W8Linear, whose GEMV reads the weights once at HBM rate."""
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        M, K = _check_bf16_rows(x, self.in_features, "x")
+        if out is None:
+            out = torch.empty((M, self.out_features), dtype=torch.bfloat16, device=x.device)
+        _check_bf16_out(out, (M, self.out_features), "out")
+        _lib.call("mj_linear_w8a8", _ptr(x), _ptr(self.q), _ptr(self.scales), _ptr(self.bias),
+                  self.epi, _ptr(out), M, self.out_features, K, _stream())
+        return out
+
+
 class W8MLP:
     """Llama-style FFN: y = ((silu(x Wg^T) * (x Wu^T)) Wd^T) on W8A16 weights.
     The gate and up projections run as one GEMM whose epilogue forms
@@ -237,5 +257,18 @@ def quantize_rowwise_int8(W: torch.Tensor, rounding: int = _lib.ROUND_RHE):
     return q, s
 
 
-__all__ = ["Linear", "ReLU", "QuantLinear", "W8Linear", "W8MLP", "quantize_rowwise_int8",
-           "_device"]
+def quantize_rows_bf16_int8(x: torch.Tensor):
+    """Per-row dynamic int8 quantize of a contiguous bf16 [M, K] device
+    tensor (the activation half of W8A8Linear); returns (xq int8 [M, K],
+    sx fp32 [M])."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous 2-D bfloat16 tensor, got {x.dtype} {list(x.shape)}")
+    M, K = x.shape
+    xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    sx = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _lib.call("mj_quantize_rows_bf16_i8", _ptr(x), M, K, _ptr(xq), _ptr(sx), _stream())
+    return xq, sx
+
+
+__all__ = ["Linear", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP",
+           "quantize_rowwise_int8", "quantize_rows_bf16_int8", "_device"]

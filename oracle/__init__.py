@@ -24,9 +24,10 @@ Parity status of each restated function (how it is pinned, see
 * quantize_symmetric_int8 / matmul_i8_i8_to_i32 / dequantize / minmax scale:
   pinned by constructed ties, the fp32-add artifact, zero rows, clamps and
   int32 brute force.
-* quantize_rowwise_rhe / linear_w8a16 / gemm_bf16_nt / mlp_w8a16: spec-only
-  (momijo has no such op); pinned by closed forms (exact ties, small-integer
-  inputs that make every sum exact) and by torch CPU cross-checks.
+* quantize_rowwise_rhe / linear_w8a16 / linear_w8a8 / gemm_bf16_nt /
+  mlp_w8a16: spec-only (momijo has no such op); pinned by closed forms (exact
+  ties, small-integer inputs that make every sum exact, power-of-two scales
+  that make the W8A8 epilogue exact) and by torch CPU cross-checks.
 """
 from __future__ import annotations
 
@@ -99,6 +100,7 @@ def _declare(L):
         "mo_quantize_rowwise_rhe": (None, [_P, _I64, _I64, _P, _P]),
         "mo_quantize_rowwise_legacy": (None, [_P, _I64, _I64, _P, _P]),
         "mo_linear_w8a16": (None, [_P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64]),
+        "mo_linear_w8a8": (None, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
         "mo_gemm_bf16_nt": (None, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64]),
         "mo_mlp_w8a16": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
         "mo_matmul_f64": (None, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64]),
@@ -438,6 +440,26 @@ def linear_w8a16(x_bf16, Q, scales, b=None, epi=EPI_NONE):
     yf = np.empty((M, N), np.float32)
     lib().mo_linear_w8a16(_ptr(x), _ptr(Q), _ptr(s), _ptr(bb), epi, _ptr(y), _ptr(yf), M, N, K)
     return y, yf
+
+
+def linear_w8a8(x_bf16, Q, scales, b=None, epi=EPI_NONE, rows=None):
+    """W8A8 Linear with per-row dynamic activation scales (momijo_oracle.c's
+    mo_linear_w8a8).  rows=(m0,m1) limits the computed rows.  Returns
+    (y_bf16 as uint16, y_f32 before rounding, xq, sx) for those rows."""
+    x = _c(x_bf16, np.uint16)
+    Q = _c(Q, np.int8)
+    s = _c(scales, np.float32)
+    M, K = x.shape
+    N = Q.shape[0]
+    m0, m1 = (0, M) if rows is None else rows
+    bb = None if b is None else _c(b, np.float32)
+    y = np.empty((m1 - m0, N), np.uint16)
+    yf = np.empty((m1 - m0, N), np.float32)
+    xq = np.empty((m1 - m0, K), np.int8)
+    sx = np.empty(m1 - m0, np.float32)
+    lib().mo_linear_w8a8(_ptr(x), _ptr(Q), _ptr(s), _ptr(bb), epi, _ptr(y), _ptr(yf), _ptr(xq),
+                         _ptr(sx), N, K, m0, m1)
+    return y, yf, xq, sx
 
 
 def gemm_bf16_nt(A_bf16, B_bf16, bias=None, epi=EPI_NONE, rows=None):

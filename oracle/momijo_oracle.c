@@ -37,6 +37,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define MO_API __attribute__((visibility("default")))
@@ -518,6 +519,43 @@ MO_API void mo_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *sca
             if (y) y[m * N + n] = mo_f32_to_bf16(v);
         }
     }
+}
+
+/* W8A8 Linear with dynamic activation scales (spec-only: the per-row /
+ * per-channel generalisation of QuantLinear.forward, learn/nn/layers.mojo:
+ * 1681-1685, whose quantize / int8 matmul / dequantize + bias steps it keeps):
+ *   row m of x upcast to fp32 (exact) and quantized by the RHE rule of
+ *   mo_quantize_rowwise_rhe -> xq[m,:], sx[m];
+ *   acc = sum_k xq[m,k] * Q[n,k] (exact integer sum);
+ *   v = (float)acc * (sx[m] * scales[n]); v = v + b[n]; y = bf16(act(v)),
+ * every fp32 operation rounded on its own.  Rows [m0, m1); xq_out / sx_out
+ * (optional) receive those rows' quantized x and scales. */
+MO_API void mo_linear_w8a8(const uint16_t *x, const int8_t *Q, const float *scales,
+                           const float *b, int epi, uint16_t *y, float *y_f32, int8_t *xq_out,
+                           float *sx_out, int64_t N, int64_t K, int64_t m0, int64_t m1) {
+    float *row = (float *)malloc((size_t)K * sizeof(float));
+    int8_t *q = (int8_t *)malloc((size_t)K);
+    if (!row || !q) { free(row); free(q); return; }
+    for (int64_t m = m0; m < m1; ++m) {
+        for (int64_t k = 0; k < K; ++k) row[k] = mo_bf16_to_f32(x[m * K + k]);
+        float sx;
+        mo_quantize_rowwise_rhe(row, 1, K, q, &sx);
+        if (xq_out) memcpy(xq_out + (m - m0) * K, q, (size_t)K);
+        if (sx_out) sx_out[m - m0] = sx;
+        for (int64_t n = 0; n < N; ++n) {
+            const int8_t *w = Q + n * K;
+            int64_t acc = 0;
+            for (int64_t k = 0; k < K; ++k) acc += (int64_t)q[k] * (int64_t)w[k];
+            const float sf = sx * scales[n];
+            float v = (float)(int32_t)acc * sf;
+            if (b) v = v + b[n];
+            v = mo_epilogue32(epi, v);
+            if (y_f32) y_f32[(m - m0) * N + n] = v;
+            if (y) y[(m - m0) * N + n] = mo_f32_to_bf16(v);
+        }
+    }
+    free(row);
+    free(q);
 }
 
 /* bf16 NT GEMM reference: momijo has no bf16 matmul (tensor/broadcast.mojo

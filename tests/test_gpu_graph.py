@@ -1,13 +1,12 @@
-"""Entry points captured into a HIP graph (torch.cuda.graph) and replayed.
+"""Entry points and HIP graph capture (torch.cuda.graph).
 
-Under capture the library cannot use its per-stream workspace (the memory
-would outlive the graph's own allocations), so the split-K W8A16 GEMM's fp32
-partials and QuantLinear's int8 copy of x become stream-ordered allocations
-that belong to the graph.  Each replay below runs on inputs rewritten in
-place since the last one, with eager work and a synchronization between
-replays, and must equal the eager result on the same inputs bit for bit
-(every kernel here sums in a fixed order).  Also covered: the M = 1 K-split
-GEMV and the bf16 GEMM.
+Calls that need the library's per-stream workspace (the split-K W8A16 GEMM,
+QuantLinear, the W8A8 Linear) are refused under capture with
+MJ_ERR_UNSUPPORTED.  test_graph_replays_match_eager is the earlier design,
+in which such calls took stream-ordered allocations owned by the graph; it
+is skipped: one run of it (with the W8A8 Linear in the captured sequence,
+after the int8 suites in the same process) faulted the GPU and the cause was
+not found, so that code path was removed.
 """
 import numpy as np
 import pytest
@@ -19,12 +18,40 @@ from _util import bf16_host_bits, to_dev
 pytestmark = pytest.mark.gpu
 
 
+def test_capture_refuses_workspace_calls(oracle, dev):
+    """A call that needs the per-stream workspace raises under capture and
+    enqueues nothing; the same call works eagerly afterwards."""
+    K = 1024
+    W = oracle.randn_f32((256, K), std=0.02, seed=81)
+    q, s = mj.quantize_rowwise_int8(to_dev(W, dev))
+    lin8 = mj.W8A8Linear(q, s)
+    x = torch.ones((64, K), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((64, 256), dtype=torch.bfloat16, device=dev)
+    lin8.forward(x, out=y)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(mj.MomijoHipError, match="graph capture"):
+        with torch.cuda.graph(graph):
+            lin8.forward(x, out=y)
+    torch.cuda.synchronize()
+    want = bf16_host_bits(y).copy()
+    y.zero_()
+    lin8.forward(x, out=y)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bf16_host_bits(y), want)
+    assert np.any(want != 0)
+
+
+@pytest.mark.skip(reason="faulted the GPU once (workspace calls captured with graph-owned "
+                         "allocations, W8A8 Linear included, run after the int8 suites); cause "
+                         "not found, and capture of workspace calls is now refused")
 def test_graph_replays_match_eager(oracle, dev):
     K = 4096
     W = oracle.randn_f32((1024, K), std=0.02, seed=71)
     q, s = mj.quantize_rowwise_int8(to_dev(W, dev))
     b = to_dev(oracle.randu_f32((1024,), -0.0625, 0.0625, seed=72), dev)
     lin = mj.W8Linear(q, s, b, mj.EPI_GELU_TANH)   # M = 64 at K = 4096: split K
+    lin8 = mj.W8A8Linear(q, s, b, mj.EPI_RELU)     # row quantize + int8 GEMM
     Wq8 = torch.randint(-127, 128, (384, 512), dtype=torch.int8, device=dev)
     ql = mj.QuantLinear(512, 384, mj.Tensor(Wq8),
                         mj.Tensor(to_dev(oracle.randu_f32((384,), -1, 1, seed=73), dev)),
@@ -37,6 +64,7 @@ def test_graph_replays_match_eager(oracle, dev):
     B = torch.empty((768, 1024), dtype=torch.bfloat16, device=dev)
     y64 = torch.empty((64, 1024), dtype=torch.bfloat16, device=dev)
     y1 = torch.empty((1, 1024), dtype=torch.bfloat16, device=dev)
+    y8 = torch.empty((64, 1024), dtype=torch.bfloat16, device=dev)
     C = torch.empty((512, 768), dtype=torch.bfloat16, device=dev)
     yq = [None]
 
@@ -49,12 +77,13 @@ def test_graph_replays_match_eager(oracle, dev):
     def run():
         lin.forward(x64, out=y64)
         lin.forward(x1, out=y1)
+        lin8.forward(x64, out=y8)
         yq[0] = ql.forward(mj.Tensor(xf)).torch
         mj.gemm_bf16_nt(A, B, out=C)
 
     def outputs():
         return [bf16_host_bits(y64), bf16_host_bits(y1), yq[0].cpu().numpy().copy(),
-                bf16_host_bits(C)]
+                bf16_host_bits(C), bf16_host_bits(y8)]
 
     # eager warm-up on a side stream (kernel attributes set, workspaces made)
     fill(0)
@@ -71,7 +100,7 @@ def test_graph_replays_match_eager(oracle, dev):
     torch.cuda.synchronize()
     graph_yq = yq[0]
 
-    names = ("W8A16 split-K GEMM", "K-split GEMV", "QuantLinear", "bf16 GEMM")
+    names = ("W8A16 split-K GEMM", "K-split GEMV", "QuantLinear", "bf16 GEMM", "W8A8 Linear")
     for rep in range(3):
         fill(rep + 1)
         torch.cuda.synchronize()

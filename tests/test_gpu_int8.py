@@ -136,12 +136,13 @@ def _exact_i8_products(A, B):
     return (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int64)
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 2048, 4096),    # 64 tiles of 256 x 256
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 4096),    # 128 tiles of 256 x 128
                                    (2000, 2100, 4112),    # partial tiles, K % 128 != 0
-                                   (512, 4096, 11008)])   # long K
+                                   (512, 4096, 11008),    # long K
+                                   (3072, 4096, 1040)])   # 192 tiles of 256 x 256, K tail
 def test_int8_gemm_large_tiles_bit_exact(dev, M, N, K):
-    """Shapes that take the 256 x 256 one-wave-per-SIMD int8 kernel: the int32
-    sums must be exact."""
+    """Shapes that take the one-wave-per-SIMD int8 kernel (256 x 256 tiles
+    from 192 of them, else 256 x 128): the int32 sums must be exact."""
     rng = np.random.default_rng(M + N + K)
     A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
     B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)

@@ -208,6 +208,83 @@ def test_w8a16_integer_inputs_exact(oracle):
     np.testing.assert_array_equal(yb, oracle.f32_to_bf16(exp))
 
 
+def test_w8a8_activation_quantize_is_rowwise_rhe(oracle):
+    """The W8A8 Linear quantizes each row of x with the per-channel RHE rule
+    applied to the exact fp32 upcast: xq, sx equal quantize_rowwise_rhe's,
+    and on a row whose absmax is 31.75 (scale 0.25 exactly) the quotients
+    (2j+1)/2 are ties that round half to even."""
+    rng = np.random.default_rng(21)
+    x = oracle.f32_to_bf16(oracle.randn_f32((5, 96), seed=22))
+    j = np.arange(-48, 48, dtype=np.float32)
+    ties = ((2 * j + 1) / 8).astype(np.float32)   # x / 0.25 = j + 0.5
+    ties[0] = -31.75                             # the absmax: scale 127 * 0.25 / 127
+    x[1] = oracle.f32_to_bf16(ties)
+    x[2] = 0                                     # zero row: scale 1, q 0
+    Q = rng.integers(-127, 128, size=(3, 96), dtype=np.int8)
+    _, _, xq, sx = oracle.linear_w8a8(x, Q, np.ones(3, np.float32))
+    q_ref, s_ref = oracle.quantize_rowwise_rhe(oracle.bf16_to_f32(x))
+    np.testing.assert_array_equal(xq, q_ref)
+    np.testing.assert_array_equal(sx, s_ref)
+    assert sx[1] == np.float32(0.25) and sx[2] == 1.0 and not xq[2].any()
+    np.testing.assert_array_equal(xq[1, 1:], np.rint(j[1:] + 0.5).astype(np.int8))
+    assert xq[1, 0] == -127
+
+
+def test_w8a8_exact_epilogue(oracle):
+    """Rows whose absmax is 127 with integer entries quantize to themselves
+    with sx = 1 exactly; power-of-two weight scales and dyadic biases then
+    make acc * sw exact, so every fp32 output is the correctly rounded value
+    of the exact acc * sw + b (computed in float64, where it is exact)."""
+    rng = np.random.default_rng(23)
+    M, N, K = 4, 24, 256
+    xi = rng.integers(-127, 128, size=(M, K)).astype(np.float32)
+    xi[:, 0] = 127
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = (2.0 ** rng.integers(-12, -6, size=N)).astype(np.float32)
+    b = (rng.integers(-64, 65, size=N) / 16).astype(np.float32)
+    for epi in (oracle.EPI_NONE, oracle.EPI_RELU):
+        yb, yf, xq, sx = oracle.linear_w8a8(oracle.f32_to_bf16(xi), Q, sw, b, epi)
+        assert (sx == 1.0).all()
+        np.testing.assert_array_equal(xq, xi.astype(np.int8))
+        acc = xi.astype(np.int64) @ Q.T.astype(np.int64)
+        exact = (acc.astype(np.float64) * sw.astype(np.float64) + b).astype(np.float32)
+        if epi == oracle.EPI_RELU:
+            exact = np.maximum(exact, 0)
+        np.testing.assert_array_equal(yf, exact)
+        np.testing.assert_array_equal(yb, oracle.f32_to_bf16(exact))
+
+
+def test_w8a8_against_torch_cpu(oracle):
+    """An independent restatement with torch CPU ops: fp32 division and
+    torch.round (half to even) for the row quantize, an int64 matmul for the
+    sums, then (acc * (sx * sw)) + b in fp32 and RNE to bf16.  Random
+    inputs, so a different scale association or rounding rule shows up."""
+    torch = pytest.importorskip("torch")
+    M, N, K = 9, 40, 200
+    x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=24))
+    x[3, 7] = oracle.f32_to_bf16(np.array([40.0], np.float32))[0]   # one outlier row
+    rng = np.random.default_rng(25)
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = oracle.randu_f32((N,), 0.0005, 0.004, seed=26)
+    b = oracle.randu_f32((N,), -0.25, 0.25, seed=27)
+    xt = torch.from_numpy(oracle.bf16_to_f32(x))
+    s = xt.abs().amax(dim=1) / 127.0
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    q = torch.clamp(torch.round(xt / s[:, None]), -127, 127).to(torch.int64)
+    acc = q @ torch.from_numpy(Q.astype(np.int64)).T
+    sf = s[:, None] * torch.from_numpy(sw)[None, :]
+    for epi in (oracle.EPI_NONE, oracle.EPI_RELU):
+        v = acc.to(torch.float32) * sf + torch.from_numpy(b)[None, :]
+        if epi == oracle.EPI_RELU:
+            v = torch.relu(v)
+        want = v.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        yb, yf, _, _ = oracle.linear_w8a8(x, Q, sw, b, epi)
+        np.testing.assert_array_equal(yf, v.numpy())
+        np.testing.assert_array_equal(yb, want)
+        yb2, _, _, _ = oracle.linear_w8a8(x, Q, sw, b, epi, rows=(2, 6))
+        np.testing.assert_array_equal(yb2, want[2:6])
+
+
 def test_mlp_fp64_composition(oracle):
     rng = np.random.default_rng(11)
     M, K, I, H = 3, 64, 48, 40
