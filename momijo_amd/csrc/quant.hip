@@ -7,7 +7,10 @@
 // registers and written as 4-byte words: the kernel touches every byte of W
 // and Q exactly once, so it is HBM-bound.  The division w/scale is the IEEE
 // correctly rounded one (built with -fhip-fp32-correctly-rounded-divide-sqrt)
-// so results are bit-identical to a CPU fp32 division.
+// so results are bit-identical to a CPU fp32 division; the RHE register paths
+// get the same integers from a multiply by 1/scale and divide only the rare
+// elements whose quotient lies within 2^-14 of a half-integer (quant_rhe_r),
+// which halves their VALU work.
 #include "common.h"
 #include "launch.h"
 
@@ -37,6 +40,48 @@ __device__ __forceinline__ int quant_rhe(float x, float scale) {
   return (int)v;
 }
 
+// quant_rhe from r = 1 / scale (correctly rounded, once per row) instead of a
+// division per element (quant4_rhe_r below).  t = x * r is within two roundings of 2^-24 each of
+// x / scale, and |x / scale| <= 127.5 (scale = max|row| / 127), so t differs
+// from the correctly rounded quotient fl(x / scale) by less than 2^-15.7:
+// rint(t) = rint(fl(x / scale)) unless one of them lies within that distance
+// of a half-integer (t - floor(t), and its distance to 0.5, are exact).
+// Those elements (about one in 8000 of random data, every element of a row of
+// exact ties) take the division.  NaN -> 0 and the scale-inf row (r = 0: every
+// finite x gives 0, as x / inf does) agree with quant_rhe; a scale whose
+// reciprocal overflows must use quant_rhe (callers check r once per row).
+// rint(x * r) and whether x is one of the elements that need the division.
+__device__ __forceinline__ float rhe_r_fast(float x, float r, bool &amb) {
+#pragma clang fp contract(off)
+  const float t = x * r;
+  const float d = t - floorf(t);
+  amb = fabsf(d - 0.5f) < 0x1p-14f;
+  return __builtin_rintf(t);
+}
+
+// A rounded quotient (NaN for a NaN input) -> int8 range, NaN -> 0.
+__device__ __forceinline__ int rhe_clamp(float v) {
+  return v != v ? 0 : (int)__builtin_amdgcn_fmed3f(v, -127.0f, 127.0f);
+}
+
+// Four elements by quant_rhe_r's rule.  The division runs only when some lane
+// of the wave holds an element that needs it (a uniform branch, taken by about
+// 3 % of the 256-element groups of random data).
+__device__ __forceinline__ void quant4_rhe_r(const float (&x)[4], float scale, float r,
+                                             int (&q)[4]) {
+  bool amb[4];
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = rhe_r_fast(x[e], r, amb[e]);
+  if (__builtin_amdgcn_ballot_w64(amb[0] | amb[1] | amb[2] | amb[3])) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (amb[e]) v[e] = __builtin_rintf(x[e] / scale);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) q[e] = rhe_clamp(v[e]);
+}
+
 // MinMaxObserver.observe's NaN rule (sequential.mojo:232-240): min and max
 // start at the first element and are replaced only when v < mn / v > mx, so
 // a NaN first element makes both NaN and later NaNs are skipped.  The
@@ -59,9 +104,17 @@ __device__ __forceinline__ float row_scale(int rounding, float amax, float mn, f
   return m / 127.0f;
 }
 
-__device__ __forceinline__ uint32_t quant4(int rounding, float4 w, float s) {
+// rounding: ROUND_RHE, ROUND_LEGACY, or kRheRecip (RHE by quant_rhe_r with
+// r = 1 / s).
+constexpr int kRheRecip = 2;
+
+__device__ __forceinline__ uint32_t quant4(int rounding, float4 w, float s, float r) {
   int q0, q1, q2, q3;
-  if (rounding == ROUND_RHE) {
+  if (rounding == kRheRecip) {
+    int q[4];
+    quant4_rhe_r({w.x, w.y, w.z, w.w}, s, r, q);
+    q0 = q[0]; q1 = q[1]; q2 = q[2]; q3 = q[3];
+  } else if (rounding == ROUND_RHE) {
     q0 = quant_rhe(w.x, s); q1 = quant_rhe(w.y, s); q2 = quant_rhe(w.z, s); q3 = quant_rhe(w.w, s);
   } else {
     q0 = quant_legacy(w.x, s); q1 = quant_legacy(w.y, s);
@@ -96,9 +149,15 @@ __global__ __launch_bounds__(256) void quantize_rowwise_reg(const float *__restr
   mx = wave_max(mx);
   observer_nan_rule(__shfl(w[0].x, 0, 64), mn, mx);
   const float s = row_scale(rounding, amax, mn, mx);
+  const float r = 1.0f / s;
   uint32_t *q4 = (uint32_t *)(Q + (size_t)row * K);
+  if (rounding == ROUND_RHE && r < __builtin_inff()) {
 #pragma unroll
-  for (int c = 0; c < CH; ++c) q4[c * 64 + lane] = quant4(rounding, w[c], s);
+    for (int c = 0; c < CH; ++c) q4[c * 64 + lane] = quant4(kRheRecip, w[c], s, r);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) q4[c * 64 + lane] = quant4(rounding, w[c], s, r);
+  }
   if (lane == 0) scales[row] = s;
 }
 
@@ -154,9 +213,9 @@ hipError_t launch_quantize_rowwise(const float *W, int64_t N, int64_t K, int rou
 // Dynamic per-row activation quantize for the W8A8 Linear: x [M, K] bf16 ->
 // xq [M, K] int8 and sx [M] fp32 with the RHE rule of quantize_rowwise
 // (scale = max|row| / 127, 1.0 for an all-zero row; q = clamp(rne(x / scale),
-// -127, 127); bf16 -> fp32 is exact).  One wave per row; for K = 512 CH
-// (CH <= 16) the row is held in registers (8 bf16 per 16-byte load), so x and
-// xq are each touched once.
+// -127, 127); bf16 -> fp32 is exact).  For K = 512 n (n <= 16) the row is
+// held in registers (8 bf16 per 16-byte load), so x and xq are each touched
+// once; other K take a two-pass kernel with one wave per row.
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
@@ -168,35 +227,67 @@ __device__ __forceinline__ float amax8(uint4 v) {
   return fmaxf(a, b);
 }
 
-__device__ __forceinline__ uint32_t quant_pair2(uint32_t w0, uint32_t w1, float s) {
-  return (uint32_t)(quant_rhe(bf16_lo(w0), s) & 0xFF) |
-         ((uint32_t)(quant_rhe(bf16_hi(w0), s) & 0xFF) << 8) |
-         ((uint32_t)(quant_rhe(bf16_lo(w1), s) & 0xFF) << 16) |
-         ((uint32_t)(quant_rhe(bf16_hi(w1), s) & 0xFF) << 24);
+template <bool RECIP>
+__device__ __forceinline__ uint32_t quant_pair2(uint32_t w0, uint32_t w1, float s, float r) {
+  const float x[4] = {bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1)};
+  int q[4];
+  if (RECIP) {
+    quant4_rhe_r(x, s, r, q);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = quant_rhe(x[e], s);
+  }
+  return (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+         ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
 }
 
-template <int CH>
+// W waves per row (W = 1, 2 or 4; 4 / W rows per workgroup), CH 16-byte
+// loads per lane: K = 512 W CH.  Several waves per row keep more loads in
+// flight than one wave holding the whole row (the kernel is latency-bound at
+// C4's 2048 rows with one); the row's absmax is combined through LDS.
+template <int W, int CH>
 __global__ __launch_bounds__(256) void quantize_rows_bf16_reg(const uint16_t *__restrict__ x,
                                                               int M, int K,
                                                               int8_t *__restrict__ xq,
                                                               float *__restrict__ sx) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ float part[4];
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const uint4 *x4 = (const uint4 *)(x + (size_t)row * K);
+  const int row = blockIdx.x * (4 / W) + wave / W;
+  const int t = (wave % W) * 64 + lane;  // lane within the row
+  const bool live = row < M;
+  const uint4 *x4 = (const uint4 *)(x + (size_t)(live ? row : 0) * K);
   uint4 v[CH];
 #pragma unroll
-  for (int c = 0; c < CH; ++c) v[c] = load_nt16(x4 + c * 64 + lane);
+  for (int c = 0; c < CH; ++c)
+    v[c] = live ? load_nt16(x4 + c * 64 * W + t) : make_uint4(0, 0, 0, 0);
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) amax = fmaxf(amax, amax8(v[c]));
   amax = wave_max(amax);
-  const float s = row_scale(ROUND_RHE, amax, 0.0f, 0.0f);
-  uint2 *q2 = (uint2 *)(xq + (size_t)row * K);
+  if (W > 1) {
+    if (lane == 0) part[wave] = amax;
+    __syncthreads();
+    const int w0 = wave - wave % W;
 #pragma unroll
-  for (int c = 0; c < CH; ++c)
-    q2[c * 64 + lane] = make_uint2(quant_pair2(v[c].x, v[c].y, s), quant_pair2(v[c].z, v[c].w, s));
-  if (lane == 0) sx[row] = s;
+    for (int w = 0; w < W; ++w) amax = fmaxf(amax, part[w0 + w]);
+  }
+  if (!live) return;
+  const float s = row_scale(ROUND_RHE, amax, 0.0f, 0.0f);
+  const float r = 1.0f / s;
+  uint2 *q2 = (uint2 *)(xq + (size_t)row * K);
+  if (r < __builtin_inff()) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      q2[c * 64 * W + t] = make_uint2(quant_pair2<true>(v[c].x, v[c].y, s, r),
+                                      quant_pair2<true>(v[c].z, v[c].w, s, r));
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      q2[c * 64 * W + t] = make_uint2(quant_pair2<false>(v[c].x, v[c].y, s, r),
+                                      quant_pair2<false>(v[c].z, v[c].w, s, r));
+  }
+  if (t == 0) sx[row] = s;
 }
 
 __global__ __launch_bounds__(256) void quantize_rows_bf16_any(const uint16_t *__restrict__ x,
@@ -215,24 +306,41 @@ __global__ __launch_bounds__(256) void quantize_rows_bf16_any(const uint16_t *__
   if (lane == 0) sx[row] = s;
 }
 
+template <int W, int CH>
+static hipError_t launch_rows_reg(const uint16_t *x, int64_t M, int64_t K, int8_t *xq, float *sx,
+                                 hipStream_t stream) {
+  const unsigned blocks = (unsigned)((M + 4 / W - 1) / (4 / W));
+  hipLaunchKernelGGL((quantize_rows_bf16_reg<W, CH>), dim3(blocks), dim3(256), 0, stream, x,
+                     (int)M, (int)K, xq, sx);
+  return hipGetLastError();
+}
+
 hipError_t launch_quantize_rows_bf16(const uint16_t *x, int64_t M, int64_t K, int8_t *xq,
                                      float *sx, hipStream_t stream) {
-  const unsigned blocks = (unsigned)((M + 3) / 4);
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)xq % 8 == 0);
   if (aligned && K % 512 == 0 && K <= 8192) {
+    // K = 512 n: 4 waves per row when n % 4 == 0, else 2 when n is even
     switch (K / 512) {
-#define MJ_QR_CASE(ch)                                                                       \
-  case ch:                                                                                   \
-    hipLaunchKernelGGL(quantize_rows_bf16_reg<ch>, dim3(blocks), dim3(256), 0, stream, x,      \
-                       (int)M, (int)K, xq, sx);                                                \
-    return hipGetLastError();
-      MJ_QR_CASE(1) MJ_QR_CASE(2) MJ_QR_CASE(3) MJ_QR_CASE(4) MJ_QR_CASE(5) MJ_QR_CASE(6)
-      MJ_QR_CASE(7) MJ_QR_CASE(8) MJ_QR_CASE(9) MJ_QR_CASE(10) MJ_QR_CASE(11) MJ_QR_CASE(12)
-      MJ_QR_CASE(13) MJ_QR_CASE(14) MJ_QR_CASE(15) MJ_QR_CASE(16)
-#undef MJ_QR_CASE
+      case 1: return launch_rows_reg<1, 1>(x, M, K, xq, sx, stream);
+      case 2: return launch_rows_reg<2, 1>(x, M, K, xq, sx, stream);
+      case 3: return launch_rows_reg<1, 3>(x, M, K, xq, sx, stream);
+      case 4: return launch_rows_reg<4, 1>(x, M, K, xq, sx, stream);
+      case 5: return launch_rows_reg<1, 5>(x, M, K, xq, sx, stream);
+      case 6: return launch_rows_reg<2, 3>(x, M, K, xq, sx, stream);
+      case 7: return launch_rows_reg<1, 7>(x, M, K, xq, sx, stream);
+      case 8: return launch_rows_reg<4, 2>(x, M, K, xq, sx, stream);
+      case 9: return launch_rows_reg<1, 9>(x, M, K, xq, sx, stream);
+      case 10: return launch_rows_reg<2, 5>(x, M, K, xq, sx, stream);
+      case 11: return launch_rows_reg<1, 11>(x, M, K, xq, sx, stream);
+      case 12: return launch_rows_reg<4, 3>(x, M, K, xq, sx, stream);
+      case 13: return launch_rows_reg<1, 13>(x, M, K, xq, sx, stream);
+      case 14: return launch_rows_reg<2, 7>(x, M, K, xq, sx, stream);
+      case 15: return launch_rows_reg<1, 15>(x, M, K, xq, sx, stream);
+      case 16: return launch_rows_reg<4, 4>(x, M, K, xq, sx, stream);
       default: break;
     }
   }
+  const unsigned blocks = (unsigned)((M + 3) / 4);
   hipLaunchKernelGGL(quantize_rows_bf16_any, dim3(blocks), dim3(256), 0, stream, x, (int)M,
                      (int)K, xq, sx);
   return hipGetLastError();

@@ -34,8 +34,10 @@ def _x_with_edges(oracle, M, K, seed):
 
 
 @pytest.mark.parametrize("M,K", [(1, 512), (5, 4096), (300, 8192), (7, 48), (3, 1000),
-                                 (2, 8704), (129, 2560)])
+                                 (2, 8704), (129, 2560), (3, 1024), (5, 3072), (6, 6144)])
 def test_quantize_rows_bf16_bit_exact(oracle, dev, M, K):
+    """Register paths with 1, 2 and 4 waves per row (K = 512 n), odd row
+    counts (a workgroup's last row past M), and the two-pass kernel."""
     x = _x_with_edges(oracle, M, K, seed=M + K)
     xq, sx = mj.quantize_rows_bf16_int8(bf16_dev(x, dev))
     q_ref, s_ref = oracle.quantize_rowwise_rhe(oracle.bf16_to_f32(x))
