@@ -290,7 +290,8 @@ def bench_c4_w8a8(steps, warmup):
         "metric": "W8A8-dynamic Linear + bias + GELU TOP/s (row quantize + int8 GEMM)",
         "value": tops, "unit": "TOP/s", "ms_per_call": ms,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": tops / PEAK_INT8_TOPS, "traffic": None},
+                     "frac": tops / PEAK_INT8_TOPS,
+                     "traffic": _traffic("c4_w8a8_dynamic_prefill_gelu_2048x4096x4096")},
     }
 
 
@@ -342,7 +343,7 @@ def bench_qlinear(steps, warmup):
         "metric": "QuantLinear (per-tensor W8A8) TOP/s, quantize + int8 GEMM + dequant",
         "value": tops, "unit": "TOP/s", "ms_per_call": ms,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": tops / PEAK_INT8_TOPS, "traffic": None},
+                     "frac": tops / PEAK_INT8_TOPS, "traffic": _traffic("quant_linear_w8a8_4096")},
     }
 
 
