@@ -226,6 +226,16 @@ int32_t mj_matmul_i8_i8_to_i32(const int8_t *A, const int8_t *B, int32_t *C,
 int32_t mj_dequantize_i32_to_f32_add_bias(const int32_t *acc, float sf, const float *b, float *y,
                                           int64_t M, int64_t N, void *stream);
 
+/* y[M,N] = float(acc) * (sx[m] * sw[n]) + b[n], each fp32 operation rounded
+ * on its own (sx * sw first); sx may be NULL (the factor is then sw[n]) and
+ * b may be NULL.  The per-channel (and per-row) form of
+ * dequantize_i32_to_f32_add_bias (learn/api/functional.mojo:281-302), for
+ * int32 sums from mj_matmul_i8_i8_to_i32 with per-channel weight scales; it
+ * is the epilogue of mj_linear_w8a8 as a separate operator. */
+int32_t mj_dequantize_i32_scaled_f32(const int32_t *acc, const float *sx, const float *sw,
+                                     const float *b, float *y, int64_t M, int64_t N,
+                                     void *stream);
+
 /* QuantLinear.forward (learn/nn/layers.mojo:1681-1685): quantize x [M,K]
  * with s_x, int8 GEMM against w_q [N,K], y = float(acc)*(s_x*s_w) + b.
  * The dequantize is fused into the GEMM epilogue; the int8 copy of x lives in
@@ -400,6 +410,10 @@ int32_t mj_matmul_i8_i8_to_i32_h(const int8_t *A, const int8_t *B, int32_t *C,
 /* dequantize_i32_to_f32_add_bias (learn/api/functional.mojo:281-302). */
 int32_t mj_dequantize_i32_to_f32_add_bias_h(const int32_t *acc, float sf, const float *b,
                                             float *y, int64_t M, int64_t N);
+/* Per-channel dequantize (see mj_dequantize_i32_scaled_f32); sx and b may be
+ * NULL. */
+int32_t mj_dequantize_i32_scaled_f32_h(const int32_t *acc, const float *sx, const float *sw,
+                                       const float *b, float *y, int64_t M, int64_t N);
 /* QuantLinear.forward (learn/nn/layers.mojo:1681-1685). */
 int32_t mj_quant_linear_f32_h(const float *x, const int8_t *Wq, const float *b,
                               float s_w, float s_x, float *y,

@@ -15,7 +15,7 @@ from .nn import (Linear, QuantLinear, ReLU, W8A8Linear, W8Linear, W8MLP, quantiz
                  quantize_rows_bf16_int8)
 from . import autograd, seam, weights
 from .autograd import GradContext, GradTensor
-from .functional import (MinMaxObserver, convert, dequantize_i32_to_f32_add_bias,
+from .functional import (MinMaxObserver, convert, dequantize_i32_scaled, dequantize_i32_to_f32_add_bias,
                          matmul_i8_i8_to_i32, prepare, quantize_symmetric_int8)
 
 __all__ = [
@@ -25,6 +25,7 @@ __all__ = [
     "Linear", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP", "quantize_rowwise_int8",
     "quantize_rows_bf16_int8",
     "quantize_symmetric_int8", "matmul_i8_i8_to_i32", "dequantize_i32_to_f32_add_bias",
+    "dequantize_i32_scaled",
     "MinMaxObserver", "prepare", "convert", "MomijoHipError", "seam", "weights",
     "autograd", "GradContext", "GradTensor",
     "EPI_NONE", "EPI_RELU", "EPI_GELU_TANH", "EPI_SILU", "EPI_GELU_TANH_APPROX",

@@ -66,6 +66,7 @@ SIGNATURES = {
     "mj_minmax_scale_symmetric": (_I32, [_P, _I64, _F, _P, _P]),
     "mj_matmul_i8_i8_to_i32": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I32, _P]),
     "mj_dequantize_i32_to_f32_add_bias": (_I32, [_P, _F, _P, _P, _I64, _I64, _P]),
+    "mj_dequantize_i32_scaled_f32": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _P]),
     "mj_quant_linear_f32": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32, _P]),
     "mj_quant_linear_f32_noalloc": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32, _P]),
     "mj_quantize_rowwise_i8": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
@@ -100,6 +101,7 @@ SIGNATURES = {
     "mj_minmax_scale_symmetric_h": (_I32, [_P, _I64, _F, _P]),
     "mj_matmul_i8_i8_to_i32_h": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I32]),
     "mj_dequantize_i32_to_f32_add_bias_h": (_I32, [_P, _F, _P, _P, _I64, _I64]),
+    "mj_dequantize_i32_scaled_f32_h": (_I32, [_P, _P, _P, _P, _P, _I64, _I64]),
     "mj_quant_linear_f32_h": (_I32, [_P, _P, _P, _F, _F, _P, _I64, _I64, _I64, _I32]),
     "mj_quantize_rowwise_i8_h": (_I32, [_P, _I64, _I64, _I32, _P, _P]),
     "mj_linear_w8a16_h": (_I32, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64]),

@@ -519,6 +519,16 @@ int32_t mj_dequantize_i32_to_f32_add_bias(const int32_t *acc, float sf, const fl
                     "dequant launch");
 }
 
+int32_t mj_dequantize_i32_scaled_f32(const int32_t *acc, const float *sx, const float *sw,
+                                     const float *b, float *y, int64_t M, int64_t N,
+                                     void *stream) {
+  if (int32_t s = check_dims(M, N, 0)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!acc || !sw || !y) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_dequant_i32_scaled(acc, sx, sw, b, y, M, N, S(stream)),
+                    "dequant_scaled launch");
+}
+
 int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, float s_w,
                             float s_x, float *y, int64_t M, int64_t N, int64_t K,
                             int32_t legacy_literal, void *stream) {

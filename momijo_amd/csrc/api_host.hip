@@ -423,6 +423,21 @@ int32_t mj_linear_w8a16_h(const uint16_t *x, const int8_t *Q, const float *scale
   });
 }
 
+int32_t mj_dequantize_i32_scaled_f32_h(const int32_t *acc, const float *sx, const float *sw,
+                                       const float *b, float *y, int64_t M, int64_t N) {
+  if (int32_t s = check_dims(M, N, 0)) return s;
+  if (M == 0 || N == 0) return MJ_OK;
+  if (!acc || !sw || !y) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[5] = {{acc, nullptr, (size_t)(M * N) * 4}, {sx, nullptr, opt_bytes(sx, (size_t)M * F4)},
+                  {sw, nullptr, (size_t)N * F4}, {b, nullptr, opt_bytes(b, (size_t)N * F4)},
+                  {nullptr, y, (size_t)(M * N) * F4}};
+  return with_device_copies(a, 5, [&](void **d) {
+    return mj_dequantize_i32_scaled_f32((const int32_t *)d[0], (const float *)d[1],
+                                        (const float *)d[2], (const float *)d[3], (float *)d[4], M,
+                                        N, nullptr);
+  });
+}
+
 int32_t mj_linear_w8a8_h(const uint16_t *x, const int8_t *Q, const float *scales,
                          const float *bias, int32_t epilogue, uint16_t *y, int64_t M, int64_t N,
                          int64_t K) {

@@ -106,6 +106,10 @@ hipError_t launch_minmax_scale(const float *x, int64_t n, float max_q, float *pa
                                float *scale_out, hipStream_t stream);
 hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b, float *y,
                                    int64_t M, int64_t N, hipStream_t stream);
+// y = float(acc) * (sx[m] * sw[n]) + b[n] (sx, b may be null).
+hipError_t launch_dequant_i32_scaled(const int32_t *acc, const float *sx, const float *sw,
+                                     const float *b, float *y, int64_t M, int64_t N,
+                                     hipStream_t stream);
 // x [M,K] bf16 -> xq [M,K] int8, sx [M] fp32: per-row RHE quantize (the W8A8
 // Linear's dynamic activation scales).
 hipError_t launch_quantize_rows_bf16(const uint16_t *x, int64_t M, int64_t K, int8_t *xq,

@@ -471,4 +471,49 @@ hipError_t launch_dequant_i32_bias(const int32_t *acc, float sf, const float *b,
   return hipGetLastError();
 }
 
+// Per-channel (and optionally per-row) dequantize of int32 sums:
+// y[m, n] = float(acc[m, n]) * (sx[m] * sw[n]) + b[n], each fp32 operation
+// rounded on its own (sx null: the factor is sw[n]; b null: no add).  The
+// W8A8 Linear's epilogue as an operator on int32 sums, and the per-channel
+// form of dequantize_i32_to_f32_add_bias (functional.mojo:281-302).  Four
+// consecutive columns per thread.
+__global__ __launch_bounds__(256) void dequant_i32_scaled_kernel(const int32_t *__restrict__ acc,
+                                                                 const float *__restrict__ sx,
+                                                                 const float *__restrict__ sw,
+                                                                 const float *__restrict__ b,
+                                                                 float *__restrict__ y, int64_t M,
+                                                                 int64_t N) {
+  const int64_t n4 = (N + 3) / 4;
+  const int64_t total = M * n4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t m = t / n4;
+    const int64_t n0 = (t - m * n4) * 4;
+    const float r = sx ? sx[m] : 1.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = n0 + q;
+      if (n >= N) break;
+      {
+#pragma clang fp contract(off)
+        const float sf = sx ? r * sw[n] : sw[n];
+        float v = (float)acc[m * N + n] * sf;
+        if (b) v = v + b[n];
+        y[m * N + n] = v;
+      }
+    }
+  }
+}
+
+hipError_t launch_dequant_i32_scaled(const int32_t *acc, const float *sx, const float *sw,
+                                     const float *b, float *y, int64_t M, int64_t N,
+                                     hipStream_t stream) {
+  int64_t blocks = (M * ((N + 3) / 4) + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(dequant_i32_scaled_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, acc,
+                     sx, sw, b, y, M, N);
+  return hipGetLastError();
+}
+
 }  // namespace mj

@@ -59,6 +59,30 @@ def dequantize_i32_to_f32_add_bias(y_i32: Tensor, sf: float, b: Tensor) -> Tenso
     return Tensor(out)
 
 
+def dequantize_i32_scaled(y_i32: Tensor, sw: Tensor, b: Tensor | None = None,
+                          sx: Tensor | None = None) -> Tensor:
+    """Per-channel form of dequantize_i32_to_f32_add_bias (functional.mojo:
+    281-302): y[m, n] = float(acc[m, n]) * (sx[m] * sw[n]) + b[n], rounded
+    step by step; sx (per-row scales) and b are optional."""
+    yt = y_i32.torch.contiguous()
+    if yt.dim() != 2 or yt.dtype != torch.int32:
+        raise ValueError(f"acc must be a 2-D int32 tensor, got {yt.dtype} {list(yt.shape)}")
+    M, N = yt.shape
+    swt = sw.torch.reshape(-1).contiguous()
+    if swt.dtype != torch.float32 or swt.numel() != N:
+        raise ValueError(f"sw must be float32 with {N} elements")
+    bt = None if b is None else b.torch.reshape(-1).contiguous()
+    if bt is not None and (bt.dtype != torch.float32 or bt.numel() != N):
+        raise ValueError(f"b must be float32 with {N} elements")
+    sxt = None if sx is None else sx.torch.reshape(-1).contiguous()
+    if sxt is not None and (sxt.dtype != torch.float32 or sxt.numel() != M):
+        raise ValueError(f"sx must be float32 with {M} elements")
+    out = torch.empty((M, N), dtype=torch.float32, device=yt.device)
+    _lib.call("mj_dequantize_i32_scaled_f32", _ptr(yt), _ptr(sxt), _ptr(swt), _ptr(bt),
+              _ptr(out), M, N, _stream())
+    return Tensor(out)
+
+
 class MinMaxObserver:
     """MinMaxObserver (sequential.mojo:217-263): running min/max, symmetric
     scale = max(|min|,|max|) / max_q (1.0 without data or for a zero range)."""

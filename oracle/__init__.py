@@ -100,6 +100,7 @@ def _declare(L):
         "mo_quantize_rowwise_rhe": (None, [_P, _I64, _I64, _P, _P]),
         "mo_quantize_rowwise_legacy": (None, [_P, _I64, _I64, _P, _P]),
         "mo_linear_w8a16": (None, [_P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64]),
+        "mo_dequant_i32_scaled": (None, [_P, _P, _P, _P, _P, _I64, _I64]),
         "mo_linear_w8a8": (None, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
         "mo_gemm_bf16_nt": (None, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64]),
         "mo_mlp_w8a16": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
@@ -388,6 +389,19 @@ def dequant_i32_bias(acc, sf: float, b) -> np.ndarray:
     M, N = acc.shape
     y = np.empty((M, N), np.float32)
     lib().mo_dequant_i32_bias(_ptr(acc), sf, _ptr(b), _ptr(y), M, N)
+    return y
+
+
+def dequant_i32_scaled(acc, sw, b=None, sx=None) -> np.ndarray:
+    """y = float(acc) * (sx[m] * sw[n]) + b[n] (momijo_oracle.c's
+    mo_dequant_i32_scaled); sx and b optional."""
+    acc = _c(acc, np.int32)
+    sw = _c(sw, np.float32)
+    b = None if b is None else _c(b, np.float32)
+    sx = None if sx is None else _c(sx, np.float32)
+    M, N = acc.shape
+    y = np.empty((M, N), np.float32)
+    lib().mo_dequant_i32_scaled(_ptr(acc), _ptr(sx), _ptr(sw), _ptr(b), _ptr(y), M, N)
     return y
 
 

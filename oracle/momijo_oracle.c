@@ -428,6 +428,21 @@ MO_API void mo_dequant_i32_bias(const int32_t *acc, float sf, const float *b, fl
         }
 }
 
+/* Per-channel (and per-row) form of dequantize_i32_to_f32_add_bias
+ * (learn/api/functional.mojo:281-302): y = float(acc) * (sx[m] * sw[n]) + b[n],
+ * sx * sw rounded first; sx NULL means the factor sw[n], b NULL no add
+ * (spec-only: the reference has the scalar-sf form above). */
+MO_API void mo_dequant_i32_scaled(const int32_t *acc, const float *sx, const float *sw,
+                                  const float *b, float *y, int64_t M, int64_t N) {
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            const float sf = sx ? sx[i] * sw[j] : sw[j];
+            float v = (float)acc[i * N + j] * sf;
+            if (b) v = v + b[j];
+            y[i * N + j] = v;
+        }
+}
+
 /* MinMaxObserver.observe + scale_symmetric (learn/api/sequential.mojo:
  * 232-263): min/max over the data, scale = max(|min|,|max|)/max_q, 1.0 when
  * there is no data, max_q <= 0 or the magnitude is 0. */

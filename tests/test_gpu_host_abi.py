@@ -197,6 +197,30 @@ def test_w8a16_h(oracle, dev):
         np.testing.assert_array_equal(y, ref)
 
 
+def test_w8a8_and_dequant_scaled_h(oracle, dev):
+    """mj_linear_w8a8_h and mj_dequantize_i32_scaled_f32_h on host buffers,
+    bit-exact against the oracle (exact int32 sums, step-by-step epilogue)."""
+    rng = np.random.default_rng(23)
+    N, K = 40, 256
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = oracle.randu_f32((N,), 0.001, 0.01, seed=24)
+    b = oracle.randu_f32((N,), -0.5, 0.5, seed=25)
+    for M, bias in ((1, b), (3, None), (300, b)):
+        x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=26 + M))
+        y = np.empty((M, N), np.uint16)
+        call("mj_linear_w8a8_h", P(x), P(Q), P(s), P(bias), mj.EPI_RELU, P(y), M, N, K)
+        ref, _, _, _ = oracle.linear_w8a8(x, Q, s, bias, mj.EPI_RELU)
+        np.testing.assert_array_equal(y, ref)
+    acc = rng.integers(-(2 ** 30), 2 ** 30, size=(19, 23)).astype(np.int32)
+    sw = oracle.randu_f32((23,), 0.001, 0.01, seed=27)
+    sx = oracle.randu_f32((19,), 0.01, 0.1, seed=28)
+    bb = oracle.randu_f32((23,), -1, 1, seed=29)
+    for rows, bias in ((sx, bb), (None, None)):
+        y = np.empty((19, 23), np.float32)
+        call("mj_dequantize_i32_scaled_f32_h", P(acc), P(rows), P(sw), P(bias), P(y), 19, 23)
+        np.testing.assert_array_equal(y, oracle.dequant_i32_scaled(acc, sw, bias, rows))
+
+
 def test_mlp_h(oracle, dev):
     M, K, I, H = 20, 256, 160, 96
     x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=21))

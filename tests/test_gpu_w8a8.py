@@ -128,6 +128,35 @@ def test_w8a8_gelu_silu_epilogue(oracle, dev, epi):
     assert float(pre.min()) < -4.0 and float(pre.max()) > 4.0 and np.mean(np.abs(pre) < 2) > 0.2
 
 
+@pytest.mark.parametrize("M,N,with_rows,with_bias", [(1, 1, True, True), (37, 1001, True, True),
+                                                    (300, 514, False, True), (5, 7, True, False)])
+def test_dequantize_i32_scaled_bit_exact(oracle, dev, M, N, with_rows, with_bias):
+    rng = np.random.default_rng(M * 7 + N)
+    acc = rng.integers(-(2 ** 31), 2 ** 31 - 1, size=(M, N)).astype(np.int32)
+    sw = oracle.randu_f32((N,), 1e-4, 1e-2, seed=N)
+    sx = oracle.randu_f32((M,), 1e-3, 1e-1, seed=M) if with_rows else None
+    b = oracle.randu_f32((N,), -1, 1, seed=N + 1) if with_bias else None
+    got = mj.dequantize_i32_scaled(mj.Tensor(to_dev(acc, dev)), mj.Tensor(to_dev(sw, dev)),
+                                   None if b is None else mj.Tensor(to_dev(b, dev)),
+                                   None if sx is None else mj.Tensor(to_dev(sx, dev))).numpy()
+    np.testing.assert_array_equal(got, oracle.dequant_i32_scaled(acc, sw, b, sx))
+
+
+def test_w8a8_is_quantize_matmul_dequantize(oracle, dev):
+    """The W8A8 Linear equals its three steps run as separate operators: the
+    row quantize, the int8 x int8 -> int32 GEMM, and the per-row/per-channel
+    dequantize + bias, rounded to bf16."""
+    M, N, K = 200, 300, 1024
+    x, Q, sw, b = _w8a8_case(oracle, M, N, K, seed=61)
+    xd, Qd = bf16_dev(x, dev), to_dev(Q, dev)
+    y = bf16_host_bits(mj.W8A8Linear(Qd, to_dev(sw, dev), to_dev(b, dev)).forward(xd))
+    xq, sx = mj.quantize_rows_bf16_int8(xd)
+    acc = mj.matmul_i8_i8_to_i32(mj.Tensor(xq), mj.Tensor(Qd).transpose())
+    yf = mj.dequantize_i32_scaled(acc, mj.Tensor(to_dev(sw, dev)), mj.Tensor(to_dev(b, dev)),
+                                  mj.Tensor(sx))
+    np.testing.assert_array_equal(y, bf16_host_bits(yf.torch.to(torch.bfloat16)))
+
+
 def test_w8a8_close_to_w8a16(oracle, dev):
     """Quantizing the activations costs at most about half an int8 step per
     element: W8A8 and W8A16 outputs of the same layer agree to a few percent

@@ -285,6 +285,28 @@ def test_w8a8_against_torch_cpu(oracle):
         np.testing.assert_array_equal(yb2, want[2:6])
 
 
+def test_dequant_scaled_closed_form(oracle):
+    """Power-of-two scales make float(acc) * (sx * sw) exact for |acc| < 2^24,
+    so y is the correctly rounded value of the exact acc * sx * sw + b; with
+    sx omitted it is the scalar rule's form per column, and with a uniform
+    sw and no sx it equals dequant_i32_bias."""
+    rng = np.random.default_rng(31)
+    M, N = 7, 33
+    acc = rng.integers(-(2 ** 23), 2 ** 23, size=(M, N)).astype(np.int32)
+    sw = (2.0 ** rng.integers(-20, -5, size=N)).astype(np.float32)
+    sx = (2.0 ** rng.integers(-6, 3, size=M)).astype(np.float32)
+    b = oracle.randu_f32((N,), -1, 1, seed=32)
+    exact = (acc.astype(np.float64) * sx[:, None].astype(np.float64) * sw.astype(np.float64)
+             + b.astype(np.float64)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.dequant_i32_scaled(acc, sw, b, sx), exact)
+    exact_nb = (acc.astype(np.float64) * sw.astype(np.float64)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.dequant_i32_scaled(acc, sw), exact_nb)
+    acc2 = rng.integers(-(2 ** 30), 2 ** 30, size=(M, N)).astype(np.int32)
+    sf = np.float32(0.0123)
+    np.testing.assert_array_equal(oracle.dequant_i32_scaled(acc2, np.full(N, sf, np.float32), b),
+                                  oracle.dequant_i32_bias(acc2, sf, b))
+
+
 def test_mlp_fp64_composition(oracle):
     rng = np.random.default_rng(11)
     M, K, I, H = 3, 64, 48, 40
