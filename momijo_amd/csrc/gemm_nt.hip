@@ -1253,7 +1253,10 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 //    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 in
 //    registers (i8x8_quarter: |q| <= 127 is exact in bf16) two MFMA groups
 //    before its MFMAs use it, at most two VALU ops beside each MFMA;
-//  * BN = 256 (waves 128 x 128), 192 (waves 128 x 96) or 128 (waves 128 x 64);
+//  * BM x BN = 256 x 256 (2 x 2 waves of 128 x 128), 256 x 192 (of 128 x 96),
+//    256 x 128 (of 128 x 64) or 128 x 256 (1 x 4 waves of 128 x 64: the same
+//    wave work as 256 x 128 from 32 KB of staged operands per stage instead
+//    of 40, since the int8 B rows cost half the bytes of the bf16 A rows);
 //    GATEUP pairs each wave's WN/2 gate rows with the WN/2 up rows of the same
 //    output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
@@ -1306,14 +1309,18 @@ __device__ __forceinline__ uint32_t i8x8_quarter_pack(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-template <int BN, bool GATEUP>
+template <int BM, int BN, bool GATEUP>
 __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
-  constexpr int BM = 256, NT = 256;
-  constexpr int WM = 128, WN = BN / 2, TM = 8, TN = WN / 16;
+  constexpr int NT = 256;
+  // waves: WMS x WNS, each owning WM x WN (2 x 2 on 256-row tiles, 1 x 4 on
+  // 128-row ones)
+  constexpr int WM = 128, WMS = BM / WM, WNS = 4 / WMS;
+  constexpr int WN = BN / WNS, TM = 8, TN = WN / 16;
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
-  constexpr int A_DPW = 8;                   // 1-KB A loads per wave per stage
+  constexpr int A_DPW = BM / 32;             // 1-KB A loads per wave per stage
   constexpr int B_DPW = BN / 64;             // 1-KB B loads per wave per stage (16 rows each)
   constexpr int BROW = 64;                   // int8 B row bytes per stage
+  static_assert(BM == 256 || BM == 128, "tile height");
   static_assert(!GATEUP || TN % 2 == 0, "gate/up pairs blocks j and j + TN/2");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t *As = lds;                                        // [2][BM][64] bf16
@@ -1322,7 +1329,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WNS, wn = wave % WNS;
   const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN_OUT - 1) / BN_OUT;
   const int tiles = tiles_m * tiles_n;
@@ -1762,19 +1769,19 @@ static hipError_t launch_w4(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BN, bool GATEUP>
+template <int BM, int BN, bool GATEUP>
 static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
-  constexpr size_t lds_loop = size_t(2) * 256 * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
-  constexpr size_t lds_out = size_t(256) * stage_ld<BN_OUT>() * sizeof(uint16_t);
+  constexpr size_t lds_loop = size_t(2) * BM * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
+  constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
   constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   static_assert(lds <= 160 * 1024, "LDS budget");
   // buffer offsets: A rows of the tile and every weight row must stay within
   // 31-bit offsets, K advances in the scalar offset
   if (p.K >= ((int64_t)1 << 30) || p.bkind != B_INT8 || p.gate_up != GATEUP ||
-      p.N * p.ldb >= ((int64_t)1 << 31) || 256 * p.lda * 2 >= ((int64_t)1 << 31))
+      p.N * p.ldb >= ((int64_t)1 << 31) || BM * p.lda * 2 >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
-  auto kern = gemm_nt_w4i8_kernel<BN, GATEUP>;
+  auto kern = gemm_nt_w4i8_kernel<BM, BN, GATEUP>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -1785,7 +1792,7 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  const int64_t grid = ((p.M + 255) / 256) * ((p.N + BN_OUT - 1) / BN_OUT) * p.splits;
+  const int64_t grid = ((p.M + BM - 1) / BM) * ((p.N + BN_OUT - 1) / BN_OUT) * p.splits;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, stream, p);
   return hipGetLastError();
@@ -1878,15 +1885,20 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     return pl;
   }
   if (w4i8_ok && p.M >= 256) {
-    // the one-wave-per-SIMD int8 kernel on 256 x 128 tiles, K split until the
-    // grid covers the 256 CUs (>= 8 stages per split).  Measured on MI355X:
-    // 2048x4096x4096 71 us (8-wave 128 x 256: 83 us; 256 x 256 tiles, which
-    // leave half the CUs idle: 126 us, split in two: 102 us); the 512 x 4096 x
-    // 11008 down projection 4-way split beats 2- and 8-way
-    pl.bm = 256;
-    pl.bn = 128;
+    // the one-wave-per-SIMD int8 kernel on 128 x 256 tiles (1 x 4 waves of
+    // 128 x 64), K split until the grid covers the 256 CUs (>= 8 stages per
+    // split).  A 128 x 256 tile stages 16 KB of bf16 A and 16 KB of int8 B per
+    // 64-deep stage where 256 x 128 (2 x 2 waves of the same shape) stages
+    // 32 KB + 8 KB for the same MFMAs: the same outputs bit for bit, 7-10 %
+    // faster at 2048x4096x4096 and 4096^3 and 5-10 % on the 4-way split
+    // 512 x 4096 x 11008 down projection (MI355X, A/B in one process).
+    // Earlier measurements: 256 x 256 tiles, which leave half the CUs idle
+    // at 2048x4096x4096: 126 us, split in two: 102 us; the 8-wave 128 x 256
+    // kernel 83 us; the down projection's 4-way split beats 2- and 8-way
+    pl.bm = 128;
+    pl.bn = 256;
     pl.wave4 = true;
-    const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
+    const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 255) / 256);
     const int64_t nk = (p.K + kBK - 1) / kBK;
     while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
       pl.splits *= 2;
@@ -1927,8 +1939,9 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.wave4) {
-      if (pl.bm != 256 || (pl.bn != 256 && pl.bn != 192)) return hipErrorInvalidValue;
-      return pl.bn == 192 ? launch_w4i8<192, true>(p, stream) : launch_w4i8<256, true>(p, stream);
+      if (pl.bm == 256 && pl.bn == 192) return launch_w4i8<256, 192, true>(p, stream);
+      if (pl.bm == 256 && pl.bn == 256) return launch_w4i8<256, 256, true>(p, stream);
+      return hipErrorInvalidValue;
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
@@ -1954,8 +1967,14 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.wave4) {
-    if (pl.bm != 256 || (pl.bn != 128 && pl.bn != 256)) return hipErrorInvalidValue;
-    e = pl.bn == 128 ? launch_w4i8<128, false>(p, stream) : launch_w4i8<256, false>(p, stream);
+    if (pl.bm == 256 && pl.bn == 128)
+      e = launch_w4i8<256, 128, false>(p, stream);
+    else if (pl.bm == 256 && pl.bn == 256)
+      e = launch_w4i8<256, 256, false>(p, stream);
+    else if (pl.bm == 128 && pl.bn == 256)
+      e = launch_w4i8<128, 256, false>(p, stream);
+    else
+      return hipErrorInvalidValue;
   } else {
     if (pl.pf2) return hipErrorInvalidValue;
     e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)

@@ -297,8 +297,8 @@ def test_c4_prefill_gelu(oracle, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 64, 256), (100, 300, 1040), (257, 520, 512),
-                                   # 256-row tiles with K % 64 != 0: a 2-way and a 4-way K
-                                   # split whose last slice ends inside a stage
+                                   # 128 x 256 tiles with K % 64 != 0: a 2-way and a 4-way
+                                   # K split whose last slice ends inside a stage
                                    (512, 384, 1040), (384, 1000, 2064)])
 def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M + N)
@@ -308,7 +308,7 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     assert normwise_rel(y, ref) <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 256 x 128 tiles, one K slice
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 128 x 256 tiles, one K slice
                                    (512, 384, 1040),     # 2-way K split, partial last stage
                                    (384, 1000, 2064),    # 4-way K split, partial N tile
                                    # skinny-M MFMA GEMV: partial 16-row tile of
@@ -336,8 +336,8 @@ def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
     in any order and under any K split, so the bf16 outputs (after scale,
     bias and rounding) must equal the oracle's bit for bit; this pins every
-    tile, fragment and swizzle index of the 256-row W8A16 kernel, of the
-    skinny-M MFMA GEMV and of the M = 1 GEMVs."""
+    tile, fragment and swizzle index of the one-wave-per-SIMD W8A16 kernel, of
+    the skinny-M MFMA GEMV and of the M = 1 GEMVs."""
     rng = np.random.default_rng(M + N + K)
     x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
     Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
