@@ -11,11 +11,12 @@
 // one-wave-per-SIMD kernel (gemm_i8_w4_kernel in gemm_nt.hip, 256 x 256 or
 // 256 x 128 tiles) cannot address a tile with 32-bit offsets (256 K >= 2^31):
 // that kernel is faster at every measured shape.  MI355X, bit-identical
-// outputs, this kernel against it: 4096^3 128.9 / 62.5 us, 3072 x 4096 x 4096
-// 93.3 / 57.4, 2048 x 4096 x 4096 66.3 / 36.8, 1024 x 4096 x 4096 50.1 / 30.7,
-// 512 x 11008 x 4096 58.5 / 33.6, 512 x 4096 x 11008 110.2 / 64.9, 1024 x
-// 1024 x 4096 40.6 / 28.3, 1000 x 3000 x 1040 21.2 / 16.8, 300 x 520 x 4112
-// 39.5 / 25.2, 512 x 512 x 4096 39.2 / 24.7.
+// outputs, settled A/B timed alternately, this kernel against it: 4096^3
+// 114.8 / 59.7 us, 3072 x 4096 x 4096 75.6 / 53.7, 2048 x 4096 x 4096 58.4 /
+// 35.3, 1024 x 4096 x 4096 47.3 / 29.9, 512 x 11008 x 4096 53.2 / 33.3,
+// 512 x 4096 x 11008 109.5 / 65.1, 1024 x 1024 x 4096 40.7 / 28.4, 1000 x
+// 3000 x 1040 20.3 / 16.4, 300 x 520 x 4112 39.7 / 25.1, 512 x 512 x 4096
+// 39.2 / 24.6.
 #include "common.h"
 #include "launch.h"
 

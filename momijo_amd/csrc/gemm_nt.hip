@@ -1889,9 +1889,9 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // 128 x 64), K split until the grid covers the 256 CUs (>= 8 stages per
     // split).  A 128 x 256 tile stages 16 KB of bf16 A and 16 KB of int8 B per
     // 64-deep stage where 256 x 128 (2 x 2 waves of the same shape) stages
-    // 32 KB + 8 KB for the same MFMAs: the same outputs bit for bit, 7-10 %
-    // faster at 2048x4096x4096 and 4096^3 and 5-10 % on the 4-way split
-    // 512 x 4096 x 11008 down projection (MI355X, A/B in one process).
+    // 32 KB + 8 KB for the same MFMAs: the same outputs bit for bit, about
+    // 1 % faster at 2048x4096x4096, 4096^3 and the 4-way split 512 x 4096 x
+    // 11008 down projection (MI355X, settled A/B in one process).
     // Earlier measurements: 256 x 256 tiles, which leave half the CUs idle
     // at 2048x4096x4096: 126 us, split in two: 102 us; the 8-wave 128 x 256
     // kernel 83 us; the down projection's 4-way split beats 2- and 8-way
