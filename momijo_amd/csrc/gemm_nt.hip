@@ -1253,12 +1253,12 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 //    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 in
 //    registers (i8x8_quarter: |q| <= 127 is exact in bf16) two MFMA groups
 //    before its MFMAs use it, at most two VALU ops beside each MFMA;
-//  * BM x BN = 256 x 256 (2 x 2 waves of 128 x 128), 256 x 192 (of 128 x 96),
-//    256 x 128 (of 128 x 64) or 128 x 256 (1 x 4 waves of 128 x 64: the same
-//    wave work as 256 x 128 from 32 KB of staged operands per stage instead
-//    of 40, since the int8 B rows cost half the bytes of the bf16 A rows);
-//    GATEUP pairs each wave's WN/2 gate rows with the WN/2 up rows of the same
-//    output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
+//  * BM x BN = 128 x 256 (1 x 4 waves of 128 x 64) for plain GEMMs: the wave
+//    work of a 256 x 128 tile from 32 KB of staged operands per stage instead
+//    of 40, since the int8 B rows cost half the bytes of the bf16 A rows; the
+//    gate/up GEMM runs 256 x 256 or 256 x 192 (2 x 2 waves of 128 x 128 or
+//    128 x 96) and pairs each wave's WN/2 gate rows with the WN/2 up rows of
+//    the same output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
 //    compiler put a full vmcnt(0) before each of them, which took away the
 //    load pipelining and doubled the kernel's time;
@@ -1967,14 +1967,8 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.wave4) {
-    if (pl.bm == 256 && pl.bn == 128)
-      e = launch_w4i8<256, 128, false>(p, stream);
-    else if (pl.bm == 256 && pl.bn == 256)
-      e = launch_w4i8<256, 256, false>(p, stream);
-    else if (pl.bm == 128 && pl.bn == 256)
-      e = launch_w4i8<128, 256, false>(p, stream);
-    else
-      return hipErrorInvalidValue;
+    if (pl.bm != 128 || pl.bn != 256) return hipErrorInvalidValue;
+    e = launch_w4i8<128, 256, false>(p, stream);
   } else {
     if (pl.pf2) return hipErrorInvalidValue;
     e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)
