@@ -520,38 +520,33 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 x bf16 256 x 256 tiles with one wave per SIMD (4 waves, 2 x 2, each a
-// 128 x 128 subtile of 64 blocks of 16 x 16).  Against the 8-wave kernel it
-// reads a third fewer LDS bytes per flop (each wave's fragments feed 128 x 128
-// outputs instead of 128 x 64), which is what pays under the power limit.
+// The tile kernels below (bf16 256 x 256 with two waves per SIMD; W8A16 and
+// int8 with one) share one pipeline:
 //
-//  * the 256 accumulator registers (64 blocks x 4) fill the accumulation
-//    register file exactly; the MFMAs are written as inline asm with the
-//    accumulator tied ("+a", D = C) so that every block stays in fixed
-//    registers (the compiler, left to itself at this pressure, rotates blocks
-//    through temporaries every iteration).  Inline asm is opaque to the hazard
+//  * the accumulators are written by inline-asm MFMAs with the accumulator
+//    tied ("+a", D = C) so that every block stays in fixed registers (the
+//    compiler, left to itself at this pressure, rotates blocks through
+//    temporaries every iteration).  Inline asm is opaque to the hazard
 //    recognizer, so the two places where other code touches the accumulators
 //    (the zero fill before the K loop and the epilogue's reads after it) are
 //    separated from the MFMAs by explicit s_nop cover; inside the loop each
-//    block is reused only every 64 MFMAs;
+//    block is reused only after the rest of its step;
 //  * K advances 64 per stage through 128-byte LDS rows (the XOR swizzle of
-//    swz()): 2 buffers for A and 3 for B, all 160 KB of LDS; every direct
-//    load fetches 128-byte row segments, half as many L2 requests as 32-deep
-//    stages would need;
-//  * each stage is two 32-deep MFMA steps, each step 8 groups of 8 MFMAs with
-//    the step's 16 fragment reads for the next step spread 3,3,3,3,2,2 over
-//    the first six groups (the last lands 16 MFMAs before the wait that needs
-//    it) and one direct load per group.  The stage's one
+//    swz()): 2 buffers for A and 3 for B; every direct load fetches 128-byte
+//    row segments, half as many L2 requests as 32-deep stages would need;
+//  * each stage is two 32-deep MFMA steps, each step one group of MFMAs per
+//    B block with the step's fragment reads for the next step spread over
+//    the first groups and one direct load per group.  The stage's one
 //    barrier sits between its two steps: there every wave holds the stage's
 //    fragments, so the stage's A buffer is free and the A loads of stage kt+2
 //    go into it during the second step; the third B buffer (stage kt-1's,
 //    free since the previous barrier) takes the B loads of stage kt+2 during
-//    the first step.  8 loads per step instead of 16 in one step: with 16 the
-//    address unit could not keep up and stalled the wave's MFMA issue;
+//    the first step.  Loads spread over both steps: 16 in one step left the
+//    address unit unable to keep up, stalling the wave's MFMA issue;
 //  * the K advance of a load is its scalar offset (no per-load VALU); the
 //    last stages, whose loads reach past K, take a per-load zero-fill select.
 //    The scalar offset stays below 2^31 and an out-of-range row offset plus it
-//    cannot wrap for K < 2^30, which the launcher checks.
+//    cannot wrap for K < 2^30, which the launchers check.
 __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, uint16_t *lds_dst,
                                        uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_dst, 16, voff, soff, 0, 0);
@@ -671,10 +666,19 @@ __device__ __forceinline__ void mfma_16x16x32_tied(f32x4 &acc, const bf16x8 &a, 
   asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-__global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
-  constexpr int BM = 256, BN = 256, NT = 256;
-  constexpr int WM = 128, WN = 128, TM = 8, TN = 8;
-  constexpr int DPO = 8;  // 1-KB direct loads per wave per operand per stage
+// bf16 256 x 256 tiles with two waves per SIMD: 8 waves laid out 2 x 4, each
+// owning 128 x 64 outputs (128 accumulator registers, so two waves fit a
+// SIMD), on the pipeline above (the 12 fragment reads of a step 3 per group,
+// one direct load per group).  A fragment read holds its wave's instruction
+// issue for about half an MFMA's 16 cycles; with one wave per SIMD (4 waves
+// of 128 x 128, the fewest reads per flop) the 16 reads of a step delayed its
+// 64 MFMAs by ~12 %, with two the other wave issues MFMAs meanwhile: 5 %
+// faster at 4096^3 in spite of 1.5x the reads per flop (MI355X, bit-identical
+// outputs).
+__global__ __launch_bounds__(512) void gemm_nt_w8_kernel(GemmNT p) {
+  constexpr int BM = 256, BN = 256, NT = 512;
+  constexpr int WM = 128, WN = 64, TM = 8, TN = 4;
+  constexpr int DPO = 4;  // 1-KB direct loads per wave per operand per stage
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t *As = lds;                    // [2][BM][64]: stage kt in buffer kt % 2
   uint16_t *Bs = lds + 2 * BM * kBK;     // [3][BN][64]: stage kt in buffer kt % 3
@@ -682,7 +686,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
   int tm, tn;
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, 4, tm, tn);
@@ -693,27 +697,24 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
                                               ((int64_t)(M - m0) * p.lda) * 2);
   const __amdgpu_buffer_rsrc_t rB = make_rsrc((const uint16_t *)p.B + (size_t)n0 * p.ldb,
                                               ((int64_t)(N - n0) * p.ldb) * 2);
-  // 1-KB block b = i*4 + wave covers tile rows [8b, 8b+8): row 8b + lane/8,
-  // stored chunk lane%8, which holds logical chunk c of the row
+  // 1-KB block b = i*8 + wave covers tile rows [8b, 8b+8)
   uint32_t a_off[DPO], b_off[DPO];
   int kc[DPO];
 #pragma unroll
   for (int i = 0; i < DPO; ++i) {
-    const int r = (i * 4 + wave) * 8 + (lane >> 3);
+    const int r = (i * 8 + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     kc[i] = c;
     a_off[i] = m0 + r < M ? (uint32_t)((r * p.lda + c * 8) * 2) : kOobOffset;
     b_off[i] = n0 + r < N ? (uint32_t)((r * p.ldb + c * 8) * 2) : kOobOffset;
   }
-  // direct load d of stage kt into buffer buf (of A for d < 8, of B
-  // otherwise): d < 8 is A block d, else B block d - 8.  FAST: the stage lies
-  // inside K.
+  // direct load d of stage kt: d < 4 is A block d, else B block d - 4
   auto load = [&](auto fast, int kt, int buf, int d) {
     const int k0 = kt * kBK;
-    const int i = d & 7;
-    uint16_t *dst = (d < 8 ? As : Bs) + buf * BM * kBK + (i * 4 + wave) * 8 * kBK;
-    const __amdgpu_buffer_rsrc_t r = d < 8 ? rA : rB;
-    const uint32_t off = d < 8 ? a_off[i] : b_off[i];
+    const int i = d & 3;
+    uint16_t *dst = (d < 4 ? As : Bs) + buf * BM * kBK + (i * 8 + wave) * 8 * kBK;
+    const __amdgpu_buffer_rsrc_t r = d < 4 ? rA : rB;
+    const uint32_t off = d < 4 ? a_off[i] : b_off[i];
     if constexpr (decltype(fast)::value) {
       dma16s(r, dst, off, (uint32_t)(k0 * 2));
     } else {
@@ -722,7 +723,6 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     }
   };
 
-  // fragment addresses of the two 32-deep steps (logical chunks 4*ks + fh)
   const int fr = lane & 15, fh = lane >> 4;
   const int sw = (fr >> 1) & 7;
   const uint16_t *a_rd[2], *b_rd[2];
@@ -744,35 +744,29 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int d = 0; d < 2 * DPO; ++d) load(std::false_type(), s, s, d);
-  __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DPO) & 0xF) | (((2 * DPO) >> 4) << 14));  // stage 0
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * DPO));  // stage 0
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
   for (int i = 0; i < TM; ++i) fa[0][i] = *(const bf16x8 *)(a_rd[0] + i * 16 * kBK);
 #pragma unroll
   for (int j = 0; j < TN; ++j) fb[0][j] = *(const bf16x8 *)(b_rd[0] + j * 16 * kBK);
-  // both ways into the K loop then arrive with no LDS read outstanding
   __builtin_amdgcn_s_waitcnt(kLgkm0);
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // zero fill -> first MFMAs
 
-  // stage kt, held in A buffer AB = kt % 2 and B buffer BB = kt % 3 (static:
-  // the loop is unrolled by six)
   auto stage = [&](auto ab_c, auto bb_c, auto fast, int kt) {
     constexpr int AB = decltype(ab_c)::value;
     constexpr int BB = decltype(bb_c)::value;
-    // the 16 fragment reads of a step go 3, 3, 3, 3, 2, 2 into groups 0-5
-    // (read t < 8: A block t, else B block t - 8), so the last lands 16 MFMAs
-    // before the wait that needs it
+    // the 12 fragment reads of a step (read t < 8: A block t, else B block
+    // t - 8) go 3 per group into groups 0-3
     auto read_frag = [&](int t, int dst, int abuf, int bbuf) {
       if (t < 8) fa[dst][t] = *(const bf16x8 *)(a_rd[dst] + abuf * BM * kBK + t * 16 * kBK);
       else fb[dst][t - 8] = *(const bf16x8 *)(b_rd[dst] + bbuf * BN * kBK + (t - 8) * 16 * kBK);
     };
     auto group = [&](int j, int src, int dst, int abuf, int bbuf, int load_d, int load_buf) {
-      const int t0 = j < 4 ? 3 * j : 12 + 2 * (j - 4);
-      const int nt = j < 4 ? 3 : (j < 6 ? 2 : 0);
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
         __builtin_amdgcn_sched_barrier(0);
-        if (u < nt) read_frag(t0 + u, dst, abuf, bbuf);
+        read_frag(3 * j + u, dst, abuf, bbuf);
         __builtin_amdgcn_sched_barrier(0);
         mfma_16x16x32_tied(acc[u][j], fb[src][j], fa[src][u]);
       }
@@ -782,21 +776,14 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
 #pragma unroll
       for (int i = 3; i < TM; ++i) mfma_16x16x32_tied(acc[i][j], fb[src][j], fa[src][i]);
     };
-    // step 0 on fa/fb[0]; read step 1 of this stage into fa/fb[1]; load B of
-    // stage kt+2 into B buffer (BB + 2) % 3, whose stage (kt-1) every wave
-    // finished reading before the previous stage's barrier
+    // step 0; B loads of stage kt+2 into B buffer (BB + 2) % 3
 #pragma unroll
-    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, 8 + j, (BB + 2) % 3);
+    for (int j = 0; j < TN; ++j) group(j, 0, 1, AB, BB, DPO + j, (BB + 2) % 3);
     __builtin_amdgcn_sched_barrier(0);
-    // this wave's reads of stage kt's buffers are done and its loads of
-    // stage kt+1 have landed (only the 8 B loads just issued may still be in
-    // flight: loads retire in order); after the barrier that holds for every
-    // wave
     __builtin_amdgcn_s_waitcnt(kLgkm0);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | 8);  // vmcnt(8)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | DPO);  // vmcnt(DPO): all but this step's B loads
     asm volatile("s_barrier" ::: "memory");
-    // step 1 on fa/fb[1]; read step 0 of stage kt+1 from the next buffers;
-    // load A of stage kt+2 into A buffer AB
+    // step 1; A loads of stage kt+2 into A buffer AB
 #pragma unroll
     for (int j = 0; j < TN; ++j) group(j, 1, 0, AB ^ 1, (BB + 1) % 3, j, AB);
     __builtin_amdgcn_sched_barrier(0);
@@ -807,7 +794,6 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   using I2 = std::integral_constant<int, 2>;
   using F = std::true_type;
   using S = std::false_type;
-  // stages kt .. kt+5 load stages kt+2 .. kt+7, inside K while kt+8 <= K/64
   const int nk_full = K / kBK;
   int kt = 0;
   for (; kt + 8 <= nk_full; kt += 6) {
@@ -818,7 +804,6 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     stage(I0(), I1(), F(), kt + 4);
     stage(I1(), I2(), F(), kt + 5);
   }
-  // the last stages (kt is a multiple of 6 here) take the zero-fill loads
   for (; kt < nk; kt += 6) {
     stage(I0(), I0(), S(), kt);
     if (kt + 1 < nk) stage(I1(), I1(), S(), kt + 1);
@@ -827,16 +812,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     if (kt + 4 < nk) stage(I0(), I1(), S(), kt + 4);
     if (kt + 5 < nk) stage(I1(), I2(), S(), kt + 5);
   }
-  // last MFMAs -> the epilogue's accumulator reads; the zero-filled loads of
-  // the two stages past the end target LDS that the epilogue reuses
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
-  if (p.part != nullptr) {  // not planned for this tile, kept complete
-    store_part8<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane, 0);
-    return;
-  }
   if (m0 + BM <= M && n0 + BN <= N && (p.ldc & 7) == 0 && ((uintptr_t)p.C & 15) == 0) {
     switch (p.epi) {
 #define MJ_DIRECT(E) store_tile_direct<E, TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane); break;
@@ -851,7 +830,6 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
     }
     return;
   }
-  // edge tiles and unaligned outputs: stage the tile in LDS, store row by row
   uint16_t *ct = lds;
   switch (p.epi) {
 #define MJ_STAGE(E) stage_tile<E, TM, TN, WM, WN, BN>(p, acc, ct, n0, wm, wn, lane); break;
@@ -868,13 +846,36 @@ __global__ __launch_bounds__(256) void gemm_nt_w4_kernel(GemmNT p) {
   flush_tile<BM, BN, NT>(p, ct, m0, n0);
 }
 
+static hipError_t launch_w8(const GemmNT &p, hipStream_t stream) {
+  constexpr size_t lds_loop = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
+  constexpr size_t lds_out = size_t(256) * stage_ld<256>() * sizeof(uint16_t);
+  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  if (p.K >= ((int64_t)1 << 30) || p.bkind != B_BF16 || p.gate_up || p.splits != 1 ||
+      256 * p.lda * 2 >= ((int64_t)1 << 31) || 256 * p.ldb * 2 >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)gemm_nt_w8_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  const int64_t grid = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_nt_w8_kernel, dim3((unsigned)grid), dim3(512), lds, stream, p);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // int8 x int8 -> int32 on 256 x BN tiles (BN = 256 or 128) with one wave per
 // SIMD: matmul_i8_i8_to_i32 (learn/api/functional.mojo:249-279), QuantLinear's
 // dequantize (learn/nn/layers.mojo:1681-1685, functional.mojo:281-302) fused
 // into the epilogue, and the W8A8 Linear with per-row activation and
 // per-channel weight scales, for problems large enough to fill the CUs.  It is
-// gemm_nt_w4_kernel's pipeline on int8 data: a 128-deep int8 stage is 128
+// the bf16 tile pipeline on int8 data: a 128-deep int8 stage is 128
 // bytes per row, the same LDS bytes as a 64-deep bf16 stage, so the buffers,
 // the XOR swizzle, the direct loads and the fragment reads are byte for byte
 // the same; a lane's 16-byte fragment of a 64-deep step is the 16 consecutive
@@ -1243,7 +1244,7 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 
 // ---------------------------------------------------------------------------
 // W8A16 tiles with one wave per SIMD: A bf16, B int8 per-channel weights.
-// The same pipeline as gemm_nt_w4_kernel (2 A buffers of 128-byte rows, 3 B
+// The bf16 tile pipeline (2 A buffers of 128-byte rows, 3 B
 // buffers, one barrier between the two 32-deep steps of a 64-deep stage, the
 // stage's direct loads spread one per MFMA group), with the weights kept int8
 // all the way into registers:
@@ -1747,28 +1748,6 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-static hipError_t launch_w4(const GemmNT &p, hipStream_t stream) {
-  constexpr size_t lds_loop = size_t(2 * 256 + 3 * 256) * kBK * sizeof(uint16_t);  // 160 KB
-  constexpr size_t lds_out = size_t(256) * stage_ld<256>() * sizeof(uint16_t);
-  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
-  static_assert(lds <= 160 * 1024, "LDS budget");
-  if (p.K >= ((int64_t)1 << 30) || p.bkind != B_BF16 || p.gate_up) return hipErrorInvalidValue;
-  static std::atomic<uint64_t> attr_set{0};
-  int dev = 0;
-  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
-    hipError_t e = hipFuncSetAttribute((const void *)gemm_nt_w4_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set.fetch_or(bit, std::memory_order_release);
-  }
-  const int64_t grid = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (grid > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm_nt_w4_kernel, dim3((unsigned)grid), dim3(256), lds, stream, p);
-  return hipGetLastError();
-}
-
 template <int BM, int BN, bool GATEUP>
 static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
@@ -1873,8 +1852,8 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // and up: 20 us faster than the 8-wave kernel)
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
-    pl.wave4 = pl.bm == 256 && w4i8_ok;
-    if (pl.wave4) {
+    pl.tile_kernel = pl.bm == 256 && w4i8_ok;
+    if (pl.tile_kernel) {
       // 192 B rows (96 output columns) when that runs fewer columns per CU:
       // rounds of 256 workgroups times columns per workgroup
       const int64_t tm = (p.M + 255) / 256;
@@ -1897,7 +1876,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // kernel 83 us; the down projection's 4-way split beats 2- and 8-way
     pl.bm = 128;
     pl.bn = 256;
-    pl.wave4 = true;
+    pl.tile_kernel = true;
     const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 255) / 256);
     const int64_t nk = (p.K + kBK - 1) / kBK;
     while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
@@ -1924,7 +1903,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     pl.pf2 = !(pl.bm == 128 && pl.bn == 128);
     // 256 x 256 runs the one-wave-per-SIMD kernel (its scalar K offsets need
     // K < 2^30; beyond that the 8-wave kernel takes the tile)
-    pl.wave4 = pl.bm == 256 && pl.bn == 256 && pl.splits == 1 && p.K < ((int64_t)1 << 30);
+    pl.tile_kernel = pl.bm == 256 && pl.bn == 256 && pl.splits == 1 && p.K < ((int64_t)1 << 30);
   } else {
     pl.iglp = !(pl.bm == 256 && pl.bn == 256);
   }
@@ -1938,7 +1917,7 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.splits = 1;
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
-    if (pl.wave4) {
+    if (pl.tile_kernel) {
       if (pl.bm == 256 && pl.bn == 192) return launch_w4i8<256, 192, true>(p, stream);
       if (pl.bm == 256 && pl.bn == 256) return launch_w4i8<256, 256, true>(p, stream);
       return hipErrorInvalidValue;
@@ -1953,9 +1932,9 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     // the bf16 schedules built: iglp with PF2 for the large tiles, iglp alone
     // for 128 x 128
     const bool small = pl.bm == 128 && pl.bn == 128;
-    if (pl.wave4) {
+    if (pl.tile_kernel) {
       if (pl.bm != 256 || pl.bn != 256 || pl.splits != 1) return hipErrorInvalidValue;
-      return launch_w4(p, stream);
+      return launch_w8(p, stream);
     }
     if (!pl.iglp || pl.pf2 == small) return hipErrorInvalidValue;
     if (small)
@@ -1966,7 +1945,7 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
       e = launch_tile<256, 128, B_BF16, false, true, true>(p, stream);
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
-  } else if (pl.wave4) {
+  } else if (pl.tile_kernel) {
     if (pl.bm != 128 || pl.bn != 256) return hipErrorInvalidValue;
     e = launch_w4i8<128, 256, false>(p, stream);
   } else {

@@ -36,13 +36,16 @@ struct GemmPlan {
   int bm = 256, bn = 256, splits = 1;
   bool iglp = false;  // K loop built with the compiler's MFMA interleave
   bool pf2 = false;   // distance-2 load pipeline (bf16 B)
-  bool wave4 = false; // one wave per SIMD: bf16 256 x 256, int8 256 x 128 / 256 x 256
+  bool tile_kernel = false;  // the dedicated tile kernels: bf16 256 x 256 (two waves per
+                             // SIMD), W8A16 128 x 256, gate/up 256 x 192 or 256 x 256
+                             // (one wave per SIMD)
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
   }
 };
 
 GemmPlan plan_gemm_nt(const GemmNT &p);
+
 hipError_t launch_gemm_nt(const GemmNT &p, const GemmPlan &plan, hipStream_t stream);
 
 // ---- gemm_f32.hip ---------------------------------------------------------
