@@ -86,8 +86,8 @@ def test_bf16_integer_inputs_bit_exact(oracle, dev):
 
 @pytest.mark.parametrize("K", [320, 200])
 def test_bf16_integer_inputs_bit_exact_256_tiles(oracle, dev, K):
-    """4096 x 4096 outputs plan onto 256 x 256 tiles (the one-wave-per-SIMD
-    kernel); K = 200 ends in a partial stage.  Sums of small integers are
+    """4096 x 4096 outputs plan onto 256 x 256 tiles (gemm_nt_w8_kernel, two
+    waves per SIMD); K = 200 ends in a partial stage.  Sums of small integers are
     exact, so every checked row must match the oracle bit for bit."""
     rng = np.random.default_rng(K)
     M = N = 4096
