@@ -1256,10 +1256,13 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 //  * a lane's B fragment of a 32-deep step is 8 int8 (one ds_read_b64 at
 //    8-byte unit (4 ks + fh) ^ 2 ((r >> 2) & 3)), widened exactly to bf16 in
 //    registers (i8x8_quarter: |q| <= 127 is exact in bf16) two MFMA groups
-//    before its MFMAs use it, at most two VALU ops beside each MFMA;
-//  * BM x BN = 128 x 256 (1 x 4 waves of 128 x 64) for plain GEMMs: the wave
-//    work of a 256 x 128 tile from 32 KB of staged operands per stage instead
-//    of 40, since the int8 B rows cost half the bytes of the bf16 A rows; the
+//    before its MFMAs use it, beside the group's last 8 MFMAs (at most two
+//    VALU ops beside each);
+//  * the widening costs one v_cvt_f32_i32 per int8, and a convert holds the
+//    wave's issue for about half of an MFMA's 16 cycles, so the wave tile is
+//    as tall as the tile: a fragment widened once feeds TM = WM / 16 MFMAs.
+//    Plain GEMMs run BM x BN = 256 x 128 with 1 x 4 waves of 256 x 32 (WMT =
+//    256: half a convert per MFMA, 18 fragment reads per 32 MFMAs); the
 //    gate/up GEMM runs 256 x 256 or 256 x 192 (2 x 2 waves of 128 x 128 or
 //    128 x 96) and pairs each wave's WN/2 gate rows with the WN/2 up rows of
 //    the same output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
@@ -1313,13 +1316,17 @@ __device__ __forceinline__ uint32_t i8x8_quarter_pack(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-template <int BM, int BN, bool GATEUP>
+template <int BM, int BN, bool GATEUP, int WMT = 128>
 __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int NT = 256;
-  // waves: WMS x WNS, each owning WM x WN (2 x 2 on 256-row tiles, 1 x 4 on
-  // 128-row ones)
-  constexpr int WM = 128, WMS = BM / WM, WNS = 4 / WMS;
-  constexpr int WN = BN / WNS, TM = 8, TN = WN / 16;
+  // waves: WMS x WNS, each owning WM x WN (WMT = 128: 2 x 2 on 256-row tiles,
+  // 1 x 4 on 128-row ones; WMT = 256: 1 x 4 on 256-row tiles)
+  constexpr int WM = WMT, WMS = BM / WM, WNS = 4 / WMS;
+  constexpr int WN = BN / WNS, TM = WM / 16, TN = WN / 16;
+  static_assert(WMT == 128 || (WMT == 256 && BM == 256 && !GATEUP), "wave tile height");
+  static_assert(TN >= 2, "the widened-fragment rotation needs two blocks per step");
+  // the B widening of a group sits beside its last 8 MFMAs
+  constexpr int CU0 = TM - 8;
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr int A_DPW = BM / 32;             // 1-KB A loads per wave per stage
   constexpr int B_DPW = BN / 64;             // 1-KB B loads per wave per stage (16 rows each)
@@ -1489,38 +1496,43 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
                            __builtin_bit_cast(bf16x8, make_uint4(fbc[cur][0], fbc[cur][1],
                                                                  fbc[cur][2], fbc[cur][3])),
                            fa[src][u]);
-        if (u == 1 || u == 2) {
-          // loads per group: ceil(nload / TN), the first at u = 1
-          const int lpg = (nload + TN - 1) / TN;
-          const int l = j * lpg + (u - 1);
-          __builtin_amdgcn_sched_barrier(0);
-          if (u - 1 < lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
-          __builtin_amdgcn_sched_barrier(0);
-        }
         {
+          // loads per group: ceil(nload / TN), at u = 1, 2, ...
+          constexpr int lpg = (nload + TN - 1) / TN;
+          static_assert(lpg < TM, "loads per group");
+          const int l = j * lpg + (u - 1);
+          if (u == 1 || u == 2 || (u >= 1 && u <= lpg)) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (u <= lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        if (u >= CU0) {
           // the fragment of group j + 2 (past the step's end: block
-          // j + 2 - TN of the next step, read at the start of this one):
-          // quarter q's two converts after MFMA 2q, its pack after MFMA 2q + 1
+          // j + 2 - TN of the next step, read in this step): quarter q's two
+          // converts after MFMA CU0 + 2q, its pack after MFMA CU0 + 2q + 1
           __builtin_amdgcn_sched_barrier(0);
-          const int q = u >> 1;
-          if (u & 1) {
+          const int q = (u - CU0) >> 1;
+          if ((u - CU0) & 1) {
             fbc[nxt][q] = i8x8_quarter_pack(cvt_lo[q], cvt_hi[q]);
           } else if (j + 2 < TN) {
             i8x8_quarter_cvt(fbr[src][j + 2], q, cvt_lo[q], cvt_hi[q]);
           } else {
             const int b = j + 2 - TN;
-            if (u == 0) {
-              // fbr[dst][b] is this step's read t = b; the t0 - b reads
-              // issued after it may still be in flight
-              if (j == TN - 2) {
-                constexpr int kAfter = ((TN - 2) * NR + TN - 1) / TN - 0;
-                static_assert(kAfter <= 15, "lgkmcnt field");
-                __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
-              } else {
-                constexpr int kAfter = ((TN - 1) * NR + TN - 1) / TN - 1;
-                static_assert(kAfter <= 15, "lgkmcnt field");
-                __builtin_amdgcn_s_waitcnt(kLgkm0 | (kAfter << 8));
-              }
+            if (u == CU0) {
+              // fbr[dst][b] is this step's read t = b; the reads issued after
+              // it up to this slot (t < min(t0 + CU0 + 1, t1)) may still be
+              // in flight (LDS reads complete in order; beyond 15 of them
+              // the wait is for a few more than needed)
+              constexpr auto k_after = [](int jj) {
+                const int tn = (jj * NR + TN - 1) / TN + CU0 + 1;
+                const int t1c = ((jj + 1) * NR + TN - 1) / TN;
+                const int after = (tn < t1c ? tn : t1c) - (jj + 2 - TN + 1);
+                return after < 15 ? after : 15;
+              };
+              static_assert(k_after(TN - 2) >= 0 && k_after(TN - 1) >= 0, "read order");
+              if (j == TN - 2) __builtin_amdgcn_s_waitcnt(kLgkm0 | (k_after(TN - 2) << 8));
+              else __builtin_amdgcn_s_waitcnt(kLgkm0 | (k_after(TN - 1) << 8));
               landed(fbr[dst][b]);
             }
             i8x8_quarter_cvt(fbr[dst][b], q, cvt_lo[q], cvt_hi[q]);
@@ -1751,7 +1763,7 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, bool GATEUP>
+template <int BM, int BN, bool GATEUP, int WMT = 128>
 static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr size_t lds_loop = size_t(2) * BM * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
@@ -1763,7 +1775,7 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   if (p.K >= ((int64_t)1 << 30) || p.bkind != B_INT8 || p.gate_up != GATEUP ||
       p.N * p.ldb >= ((int64_t)1 << 31) || BM * p.lda * 2 >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
-  auto kern = gemm_nt_w4i8_kernel<BM, BN, GATEUP>;
+  auto kern = gemm_nt_w4i8_kernel<BM, BN, GATEUP, WMT>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -1867,20 +1879,22 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     return pl;
   }
   if (w4i8_ok && p.M >= 256) {
-    // the one-wave-per-SIMD int8 kernel on 128 x 256 tiles (1 x 4 waves of
-    // 128 x 64), K split until the grid covers the 256 CUs (>= 8 stages per
-    // split).  A 128 x 256 tile stages 16 KB of bf16 A and 16 KB of int8 B per
-    // 64-deep stage where 256 x 128 (2 x 2 waves of the same shape) stages
-    // 32 KB + 8 KB for the same MFMAs: the same outputs bit for bit, about
-    // 1 % faster at 2048x4096x4096, 4096^3 and the 4-way split 512 x 4096 x
-    // 11008 down projection (MI355X, settled A/B in one process).
+    // the one-wave-per-SIMD int8 kernel on 256 x 128 tiles with 1 x 4 waves of
+    // 256 x 32, K split until the grid covers the 256 CUs (>= 8 stages per
+    // split).  A widened B fragment feeds 16 MFMAs instead of 8, which halves
+    // the int8 -> bf16 converts per MFMA (a v_cvt_f32_i32 holds a wave's issue
+    // for about half an MFMA); the cost is 18 fragment reads per 32 MFMAs
+    // instead of 12.  Bit-identical outputs, 5.5 % faster at 2048x4096x4096,
+    // 2.9 % at the 4-way split 512 x 4096 x 11008 down projection and 5.2 % at
+    // 4096^3 than 128 x 256 tiles of 1 x 4 waves of 128 x 64 (MI355X, settled
+    // A/B in one process).
     // Earlier measurements: 256 x 256 tiles, which leave half the CUs idle
     // at 2048x4096x4096: 126 us, split in two: 102 us; the 8-wave 128 x 256
     // kernel 83 us; the down projection's 4-way split beats 2- and 8-way
-    pl.bm = 128;
-    pl.bn = 256;
+    pl.bm = 256;
+    pl.bn = 128;
     pl.tile_kernel = true;
-    const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 255) / 256);
+    const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
     const int64_t nk = (p.K + kBK - 1) / kBK;
     while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
       pl.splits *= 2;
@@ -1949,8 +1963,8 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.tile_kernel) {
-    if (pl.bm != 128 || pl.bn != 256) return hipErrorInvalidValue;
-    e = launch_w4i8<128, 256, false>(p, stream);
+    if (pl.bm != 256 || pl.bn != 128) return hipErrorInvalidValue;
+    e = launch_w4i8<256, 128, false, 256>(p, stream);
   } else {
     if (pl.pf2) return hipErrorInvalidValue;
     e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)

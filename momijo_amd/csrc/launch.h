@@ -37,7 +37,7 @@ struct GemmPlan {
   bool iglp = false;  // K loop built with the compiler's MFMA interleave
   bool pf2 = false;   // distance-2 load pipeline (bf16 B)
   bool tile_kernel = false;  // the dedicated tile kernels: bf16 256 x 256 (two waves per
-                             // SIMD), W8A16 128 x 256, gate/up 256 x 192 or 256 x 256
+                             // SIMD), W8A16 256 x 128, gate/up 256 x 192 or 256 x 256
                              // (one wave per SIMD)
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;

@@ -297,9 +297,10 @@ def test_c4_prefill_gelu(oracle, dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 64, 256), (100, 300, 1040), (257, 520, 512),
-                                   # 128 x 256 tiles with K % 64 != 0: a 2-way and a 4-way
-                                   # K split whose last slice ends inside a stage
-                                   (512, 384, 1040), (384, 1000, 2064)])
+                                   # 256 x 128 tiles (waves of 256 x 32) with K % 64 != 0: a
+                                   # 2-way and a 4-way K split whose last slice ends inside a
+                                   # stage, and partial tiles in M and N
+                                   (512, 384, 1040), (384, 1000, 2064), (1000, 1300, 528)])
 def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M + N)
     lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_RELU)
@@ -308,9 +309,10 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
     assert normwise_rel(y, ref) <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 128 x 256 tiles, one K slice
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512),      # 256 x 128 tiles, one K slice
                                    (512, 384, 1040),     # 2-way K split, partial last stage
                                    (384, 1000, 2064),    # 4-way K split, partial N tile
+                                   (1000, 1300, 528),    # partial M and N tiles, one K slice
                                    # skinny-M MFMA GEMV: partial 16-row tile of
                                    # weights, K % 64 != 0, x rows < 16
                                    (3, 4104, 1040), (16, 1000, 4096),
@@ -336,7 +338,7 @@ def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
     in any order and under any K split, so the bf16 outputs (after scale,
     bias and rounding) must equal the oracle's bit for bit; this pins every
-    tile, fragment and swizzle index of the one-wave-per-SIMD W8A16 kernel, of
+    tile, fragment and swizzle index of the one-wave-per-SIMD W8A16 kernels, of
     the skinny-M MFMA GEMV and of the M = 1 GEMVs."""
     rng = np.random.default_rng(M + N + K)
     x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
@@ -347,6 +349,26 @@ def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     y = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
     ref, _ = oracle.linear_w8a16(x, Q, s, b, mj.EPI_NONE)
     np.testing.assert_array_equal(y, ref)
+
+
+def test_w8a16_integer_inputs_bit_exact_c4_shape(oracle, dev):
+    """C4's 2048 x 4096 x 4096 on exact integer sums: every checked row (two
+    or more in each of the eight 256-row tiles, at fragment and tile edges)
+    must equal the oracle bit for bit over all 4096 columns, i.e. every
+    column tile of the 256 x 128 W8A16 tiles."""
+    M, N, K = 2048, 4096, 4096
+    rng = np.random.default_rng(2048)
+    x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, size=N)).astype(np.float32)
+    b = rng.integers(-8, 9, size=N).astype(np.float32) / np.float32(4)
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), to_dev(b, dev), mj.EPI_NONE)
+    y = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
+    rows = [0, 1, 15, 16, 255, 256, 300, 511, 512, 700, 767, 768, 1023, 1024, 1300, 1535,
+            1536, 1800, 1791, 1792, 2046, 2047]
+    for r in rows:
+        ref, _ = oracle.linear_w8a16(x[r:r + 1], Q, s, b, mj.EPI_NONE)
+        np.testing.assert_array_equal(y[r:r + 1], ref, err_msg=f"row {r}")
 
 
 @pytest.mark.parametrize("M", [1, 5, 12, 40, 256])
