@@ -1263,9 +1263,12 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 //    as tall as the tile: a fragment widened once feeds TM = WM / 16 MFMAs.
 //    Plain GEMMs run BM x BN = 256 x 128 with 1 x 4 waves of 256 x 32 (WMT =
 //    256: half a convert per MFMA, 18 fragment reads per 32 MFMAs); the
-//    gate/up GEMM runs 256 x 256 or 256 x 192 (2 x 2 waves of 128 x 128 or
-//    128 x 96) and pairs each wave's WN/2 gate rows with the WN/2 up rows of
-//    the same output columns (blocks j and j + TN/2), as gemm_nt_kernel does;
+//    gate/up GEMM runs 256 x 192 or 256 x 256 with 1 x 4 waves of 256 x 48 or
+//    256 x 64, waves 0-1 on the tile's gate rows and waves 2-3 on the up rows
+//    of the same output columns, paired through LDS in the epilogue
+//    (gateup_split_epilogue).  With WMT = 128 (2 x 2 or 1 x 4 waves of 128
+//    rows, the layout these replaced) a gate/up wave pairs its own WN/2 gate
+//    and WN/2 up rows (blocks j and j + TN/2), as gemm_nt_kernel does;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
 //    compiler put a full vmcnt(0) before each of them, which took away the
 //    load pipelining and doubled the kernel's time;
@@ -1316,6 +1319,124 @@ __device__ __forceinline__ uint32_t i8x8_quarter_pack(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+// Gate/up epilogue of the split layout (1 x 4 waves of 256 x WN): wave wn < 2
+// holds the gate sums of output columns [wn WN, wn WN + WN) of the tile, wave
+// wn + 2 the up sums of the same columns, for all 256 rows.  Each side scales
+// its sums (g = acc * sg, u = acc * su, as the paired layout) and hands one
+// half of the rows to its partner through its own LDS region (the gate waves
+// rows 0-127 into xs[0], the up waves rows 128-255 into xs[1], each 128 rows
+// of the tile's 2 WN columns in fp32); then the up waves finish rows 0-127 and
+// the gate waves rows 128-255: h = silu_b16(g) * u in bf16, the same
+// arithmetic as the paired layout.  Full tiles are stored from registers;
+// partial ones are staged through LDS (after every wave has read xs) and
+// written by flush_tile.  The LDS is free on entry (every wave has passed the
+// K loop's last barrier).
+template <int TM, int TN, int WN>
+__device__ __forceinline__ void gateup_split_epilogue(const GemmNT &p, const f32x4 (&acc)[TM][TN],
+                                                      float *xs, int m0, int n0, int wn, int lane,
+                                                      bool full) {
+  constexpr int HM = TM / 2;            // row blocks handed over / kept
+  constexpr int LDX = 2 * WN + 4;       // fp32 row stride of the exchange regions
+  const int N = (int)p.N;
+  const int fr = lane & 15, fh = lane >> 4;
+  const bool up = wn >= 2;
+  const int cw = (up ? wn - 2 : wn) * WN;  // the wave's first output column in the tile
+  float sc[TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + cw + j * 16 + 4 * fh + q;
+      const int nc = n < N ? n : N - 1;
+      sc[j][q] = up ? p.scales2[nc] : p.scales[nc];
+    }
+  // the accumulator row block indices must be compile-time constants (a
+  // runtime index would move the accumulators to scratch), hence one body
+  // per side
+  auto run = [&](auto up_c) {
+    constexpr bool UP = decltype(up_c)::value;
+    constexpr int send0 = UP ? HM : 0, keep0 = UP ? 0 : HM;
+#pragma unroll
+    for (int i = 0; i < HM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        f32x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+          v[q] = acc[send0 + i][j][q] * sc[j][q];
+        }
+        *(f32x4 *)(xs + ((UP ? 128 : 0) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh) = v;
+      }
+    __syncthreads();
+    // h of row block keep0 + i, column block j (4 values of one lane), the
+    // partner's half from the other region
+    auto h4 = [&](int i, int j, float (&h)[4]) {
+      const f32x4 o =
+          *(const f32x4 *)(xs + ((UP ? 0 : 128) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+        const float own = acc[keep0 + i][j][q] * sc[j][q];
+        const float g = UP ? o[q] : own;
+        const float u = UP ? own : o[q];
+        h[q] = silu_b16(g) * u;
+      }
+    };
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < HM; ++i) {
+        const int m = m0 + (keep0 + i) * 16 + fr;
+#pragma unroll
+        for (int j = 0; j + 1 < TN; j += 2) {
+          float x[4], y[4];
+          h4(i, j, x);
+          h4(i, j + 1, y);
+          const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
+                                                           pack_bf16x2(y[0], y[1]), false, false);
+          const auto w1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[2], x[3]),
+                                                           pack_bf16x2(y[2], y[3]), false, false);
+          const int n = n0 + cw + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
+          *(uint4 *)(p.C + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
+        }
+        if constexpr (TN % 2 == 1) {
+          float h[4];
+          h4(i, TN - 1, h);
+          const int n = n0 + cw + (TN - 1) * 16 + 4 * fh;
+          *(uint2 *)(p.C + (size_t)m * p.ldc + n) = make_uint2(pack_bf16x2(h[0], h[1]),
+                                                               pack_bf16x2(h[2], h[3]));
+        }
+      }
+      return;
+    }
+    // partial tile: h as bf16 in registers, then (once every wave has read
+    // xs) into the staging tile over it
+    uint32_t hp[HM][TN][2];
+#pragma unroll
+    for (int i = 0; i < HM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float h[4];
+        h4(i, j, h);
+        hp[i][j][0] = pack_bf16x2(h[0], h[1]);
+        hp[i][j][1] = pack_bf16x2(h[2], h[3]);
+      }
+    __syncthreads();
+    constexpr int LD = stage_ld<2 * WN>();
+    uint16_t *ct = (uint16_t *)xs;
+#pragma unroll
+    for (int i = 0; i < HM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *(uint2 *)(ct + ((keep0 + i) * 16 + fr) * LD + cw + j * 16 + 4 * fh) =
+            make_uint2(hp[i][j][0], hp[i][j][1]);
+    __syncthreads();
+    flush_tile<TM * 16, 2 * WN, 256>(p, ct, m0, n0);
+  };
+  if (up) run(std::true_type());
+  else run(std::false_type());
+}
+
 template <int BM, int BN, bool GATEUP, int WMT = 128>
 __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int NT = 256;
@@ -1323,7 +1444,12 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   // 1 x 4 on 128-row ones; WMT = 256: 1 x 4 on 256-row tiles)
   constexpr int WM = WMT, WMS = BM / WM, WNS = 4 / WMS;
   constexpr int WN = BN / WNS, TM = WM / 16, TN = WN / 16;
-  static_assert(WMT == 128 || (WMT == 256 && BM == 256 && !GATEUP), "wave tile height");
+  static_assert(WMT == 128 || (WMT == 256 && BM == 256), "wave tile height");
+  // gate/up with WMT = 256: the tile's B rows are BN/2 gate rows then the BN/2
+  // up rows of the same output columns, so waves 0-1 hold gate sums and waves
+  // 2-3 the up sums of the same columns (paired in the epilogue through LDS);
+  // with WMT = 128 each wave pairs its own blocks j and j + TN/2
+  constexpr bool SPLITGU = GATEUP && WMT == 256;
   static_assert(TN >= 2, "the widened-fragment rotation needs two blocks per step");
   // the B widening of a group sits beside its last 8 MFMAs
   constexpr int CU0 = TM - 8;
@@ -1332,7 +1458,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int B_DPW = BN / 64;             // 1-KB B loads per wave per stage (16 rows each)
   constexpr int BROW = 64;                   // int8 B row bytes per stage
   static_assert(BM == 256 || BM == 128, "tile height");
-  static_assert(!GATEUP || TN % 2 == 0, "gate/up pairs blocks j and j + TN/2");
+  static_assert(!GATEUP || SPLITGU || TN % 2 == 0, "gate/up pairs blocks j and j + TN/2");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t *As = lds;                                        // [2][BM][64] bf16
   int8_t *Bs = (int8_t *)(lds + 2 * BM * kBK);               // [3][BN][64] int8
@@ -1378,7 +1504,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     int n = n0 + r;
     b_up[i] = false;
-    if (GATEUP) {
+    if (SPLITGU) {
+      b_up[i] = r >= BN / 2;
+      n = n0 + (b_up[i] ? r - BN / 2 : r);
+    } else if (GATEUP) {
       const int w = r / WN, rr = r % WN;
       b_up[i] = rr >= WN / 2;
       n = n0 + w * (WN / 2) + rr % (WN / 2);
@@ -1601,7 +1730,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   }
   const bool full = m0 + BM <= M && n0 + BN_OUT <= N && (p.ldc & 7) == 0 &&
                     ((uintptr_t)p.C & 15) == 0;
-  if constexpr (GATEUP) {
+  if constexpr (SPLITGU) {
+    gateup_split_epilogue<TM, TN, WN>(p, acc, (float *)lds, m0, n0, wn, lane, full);
+    return;
+  } else if constexpr (GATEUP) {
     if (full) {
       store_gateup_direct<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane);
       return;
@@ -1768,7 +1900,10 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
   constexpr size_t lds_loop = size_t(2) * BM * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
   constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
-  constexpr size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  // the split gate/up epilogue's two fp32 exchange regions (128 rows each)
+  constexpr size_t lds_x = (GATEUP && WMT == 256) ? size_t(2) * 128 * (BN_OUT + 4) * 4 : 0;
+  constexpr size_t lds_lo = lds_loop > lds_out ? lds_loop : lds_out;
+  constexpr size_t lds = lds_lo > lds_x ? lds_lo : lds_x;
   static_assert(lds <= 160 * 1024, "LDS budget");
   // buffer offsets: A rows of the tile and every weight row must stay within
   // 31-bit offsets, K advances in the scalar offset
@@ -1864,11 +1999,18 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   if (p.gate_up) {
     // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up.
     // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
-    // and up: 20 us faster than the 8-wave kernel)
+    // and up: 20 us faster than the 8-wave kernel) in its split layout: 1 x 4
+    // waves of 256 x BN/4, gate rows in waves 0-1 and the up rows of the same
+    // columns in waves 2-3, paired through LDS in the epilogue.  A widened
+    // fragment then feeds 16 MFMAs instead of 8 (2 x 2 waves of 128 x BN/2,
+    // each pairing its own gate and up blocks): bit-identical, C5's gate/up
+    // 78.6 -> 68.1 us, 1024 x 4096 x 4096 73.7 -> 61.2 us (MI355X, settled A/B
+    // in one process)
     pl.bm = p.M > 128 ? 256 : 128;
     pl.bn = 256;
     pl.tile_kernel = pl.bm == 256 && w4i8_ok;
     if (pl.tile_kernel) {
+      pl.wm = 256;
       // 192 B rows (96 output columns) when that runs fewer columns per CU:
       // rounds of 256 workgroups times columns per workgroup
       const int64_t tm = (p.M + 255) / 256;
@@ -1893,6 +2035,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // kernel 83 us; the down projection's 4-way split beats 2- and 8-way
     pl.bm = 256;
     pl.bn = 128;
+    pl.wm = 256;
     pl.tile_kernel = true;
     const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
     const int64_t nk = (p.K + kBK - 1) / kBK;
@@ -1935,8 +2078,9 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.tile_kernel) {
-      if (pl.bm == 256 && pl.bn == 192) return launch_w4i8<256, 192, true>(p, stream);
-      if (pl.bm == 256 && pl.bn == 256) return launch_w4i8<256, 256, true>(p, stream);
+      if (pl.bm != 256 || pl.wm != 256) return hipErrorInvalidValue;
+      if (pl.bn == 192) return launch_w4i8<256, 192, true, 256>(p, stream);
+      if (pl.bn == 256) return launch_w4i8<256, 256, true, 256>(p, stream);
       return hipErrorInvalidValue;
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
@@ -1963,7 +2107,7 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.tile_kernel) {
-    if (pl.bm != 256 || pl.bn != 128) return hipErrorInvalidValue;
+    if (pl.bm != 256 || pl.bn != 128 || pl.wm != 256) return hipErrorInvalidValue;
     e = launch_w4i8<256, 128, false, 256>(p, stream);
   } else {
     if (pl.pf2) return hipErrorInvalidValue;

@@ -39,6 +39,9 @@ struct GemmPlan {
   bool tile_kernel = false;  // the dedicated tile kernels: bf16 256 x 256 (two waves per
                              // SIMD), W8A16 256 x 128, gate/up 256 x 192 or 256 x 256
                              // (one wave per SIMD)
+  int wm = 128;              // W8A16 tile kernels: wave tile height; the planner sets 256
+                             // (1 x 4 waves of 256 rows: each widened B fragment feeds 16
+                             // MFMAs)
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
   }

@@ -458,6 +458,37 @@ def test_c5_mlp(oracle, dev):
     assert worst_h <= BF16_TOL and worst_y <= BF16_TOL
 
 
+@pytest.mark.parametrize("M,K,I", [(512, 1024, 2000),   # 2 row tiles, partial last column tile
+                                   (300, 528, 400),     # partial row tile, K % 64 != 0
+                                   (1024, 256, 4096),   # 4 x 43 tiles, one K slice of 4 stages
+                                   (257, 64, 112)])     # one-row second tile, one stage
+def test_mlp_gateup_integer_sums(oracle, dev, M, K, I):
+    """The gate/up GEMM on exact sums: small-integer x, int8 weights and
+    power-of-two scales make g = x Wg^T sg and u = x Wu^T su exact in fp32, so
+    every h = silu(g) u must lie within one bf16 step (2^-8 relative, or 1e-6
+    absolute) of the float64 value from those exact sums.  A wrong pairing of
+    gate and up rows, a swapped exchange half or a shifted column of the
+    split layout's epilogue (gate sums in waves 0-1, up sums in waves 2-3,
+    paired through LDS) is off by far more."""
+    rng = np.random.default_rng(M + K + I)
+    x = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
+    Wg = rng.integers(-127, 128, size=(I, K), dtype=np.int8)
+    Wu = rng.integers(-127, 128, size=(I, K), dtype=np.int8)
+    sg = (2.0 ** rng.integers(-14, -10, size=I)).astype(np.float32)
+    su = (2.0 ** rng.integers(-14, -10, size=I)).astype(np.float32)
+    Wd = rng.integers(-127, 128, size=(64, I), dtype=np.int8)
+    sd = np.full(64, 2.0 ** -20, np.float32)
+    _, h = _run_mlp(dev, x, Wg, sg, Wu, su, Wd, sd)
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    g = (xf @ Wg.astype(np.float64).T) * sg.astype(np.float64)
+    u = (xf @ Wu.astype(np.float64).T) * su.astype(np.float64)
+    ref = g / (1.0 + np.exp(-g)) * u
+    err = np.abs(h.astype(np.float64) - ref)
+    bound = np.maximum(np.abs(ref) * 2.0 ** -8, 1e-6)
+    bad = np.argwhere(err > bound)
+    assert bad.size == 0, f"{len(bad)} outputs off, first at {bad[0]}: {h[tuple(bad[0])]} vs {ref[tuple(bad[0])]}"
+
+
 @pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (12, 256, 400, 130), (40, 512, 256, 320), (300, 256, 528, 64),
                                      # gate/up on 192-row tiles (a partial one), K % 64 != 0
                                      (384, 1040, 400, 272)])
