@@ -228,8 +228,12 @@ __device__ __forceinline__ float wave_min(float v) {
 __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int group_m,
                                             int &tm, int &tn) {
   const int total = tiles_m * tiles_n;
-  int logical = bid;
-  if ((total & 7) == 0) logical = (bid & 7) * (total >> 3) + (bid >> 3);
+  // workgroup bid runs on XCD bid % 8; XCD x takes the contiguous logical
+  // range [x q + min(x, r), ...) of c_x = q + (x < r) tiles (q = total / 8,
+  // r = total % 8), so neighbouring tiles, which share operand panels, share
+  // an L2
+  const int x = bid & 7, q = total >> 3, r = total & 7;
+  const int logical = x * q + (x < r ? x : r) + (bid >> 3);
   const int per_group = group_m * tiles_n;
   const int g = logical / per_group;
   const int first_m = g * group_m;
