@@ -225,6 +225,20 @@ __device__ __forceinline__ float wave_min(float v) {
 // compact block of tiles that shares A rows and B rows in that XCD's L2:
 // the ids are first regrouped per XCD, then walked GROUP_M tile rows at a
 // time, column by column.
+// The walk: logical tile index -> (tile_m, tile_n), GROUP_M tile rows at a
+// time, column by column.
+__device__ __forceinline__ void group_coords(int logical, int tiles_m, int tiles_n, int group_m,
+                                             int &tm, int &tn) {
+  const int per_group = group_m * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * group_m;
+  int gsize = tiles_m - first_m;
+  if (gsize > group_m) gsize = group_m;
+  const int in_g = logical - g * per_group;
+  tm = first_m + in_g % gsize;
+  tn = in_g / gsize;
+}
+
 __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int group_m,
                                             int &tm, int &tn) {
   const int total = tiles_m * tiles_n;
@@ -234,14 +248,24 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   // an L2
   const int x = bid & 7, q = total >> 3, r = total & 7;
   const int logical = x * q + (x < r ? x : r) + (bid >> 3);
-  const int per_group = group_m * tiles_n;
-  const int g = logical / per_group;
-  const int first_m = g * group_m;
-  int gsize = tiles_m - first_m;
-  if (gsize > group_m) gsize = group_m;
-  const int in_g = logical - g * per_group;
-  tm = first_m + in_g % gsize;
-  tn = in_g / gsize;
+  group_coords(logical, tiles_m, tiles_n, group_m, tm, tn);
+}
+
+// Split-K grids of `splits` K slices of `tiles` tiles: when splits divides 8
+// and the grid is a multiple of 8, XCD x runs K slice x / (8 / splits), so
+// the A and B panels of a slice are fetched by 8 / splits XCDs instead of
+// all eight; otherwise slice-major order with tile_coords within a slice.
+__device__ __forceinline__ void split_tile_coords(int bid, int tiles_m, int tiles_n, int splits,
+                                                  int group_m, int &split, int &tm, int &tn) {
+  const int tiles = tiles_m * tiles_n;
+  if (splits > 1 && (8 % splits) == 0 && ((tiles * splits) & 7) == 0) {
+    const int xs = 8 / splits, x = bid & 7;
+    split = x / xs;
+    group_coords((x % xs) * (tiles / xs) + (bid >> 3), tiles_m, tiles_n, group_m, tm, tn);
+    return;
+  }
+  split = bid / tiles;
+  tile_coords(bid - split * tiles, tiles_m, tiles_n, group_m, tm, tn);
 }
 
 }  // namespace mj

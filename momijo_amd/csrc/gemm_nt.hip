@@ -302,10 +302,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_kernel(GemmNT p) {
   const int M = (int)p.M, N = (int)p.N;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN_OUT - 1) / BN_OUT;
-  const int tiles = tiles_m * tiles_n;
-  const int split = blockIdx.x / tiles;
-  int tm, tn;
-  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, 4, tm, tn);
+  int split, tm, tn;
+  split_tile_coords(blockIdx.x, tiles_m, tiles_n, p.splits, 4, split, tm, tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN_OUT;
   // this workgroup's K slice: stages [kt0, kt1); loads stop at K (edge) or at
@@ -1469,10 +1467,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   const int wm = wave / WNS, wn = wave % WNS;
   const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN_OUT - 1) / BN_OUT;
-  const int tiles = tiles_m * tiles_n;
-  const int split = blockIdx.x / tiles;
-  int tm, tn;
-  tile_coords(blockIdx.x - split * tiles, tiles_m, tiles_n, 4, tm, tn);
+  int split, tm, tn;
+  split_tile_coords(blockIdx.x, tiles_m, tiles_n, p.splits, 4, split, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN_OUT;
   const int nk_all = (K + kBK - 1) / kBK;
   const int per = (nk_all + p.splits - 1) / p.splits;
