@@ -597,65 +597,6 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
   }
 }
 
-// Gate/up epilogue of a full, aligned tile straight from the accumulators:
-// h = silu(g*sg) * (u*su) (silu_b16) for blocks j < TN/2 (gate) and j + TN/2 (up),
-// then the same permlane pairing as store_tile_direct over the TN/2 output
-// blocks, row block by row block; an odd last block is stored 8 bytes (4
-// columns) per lane.
-template <int TM, int TN, int WM, int WN>
-__device__ __forceinline__ void store_gateup_direct(const GemmNT &p, const f32x4 (&acc)[TM][TN],
-                                                    int m0, int n0, int wm, int wn, int lane) {
-  constexpr int TO = TN / 2;
-  const int fr = lane & 15, fh = lane >> 4;
-  float sg[TO][4], su[TO][4];
-#pragma unroll
-  for (int j = 0; j < TO; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = n0 + wn * (WN / 2) + j * 16 + 4 * fh + q;
-      sg[j][q] = p.scales[n];
-      su[j][q] = p.scales2[n];
-    }
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WM + i * 16 + fr;
-#pragma unroll
-    for (int j = 0; j + 1 < TO; j += 2) {
-      float x[4], y[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma clang fp contract(off)
-        const float g0 = epi_scale_bias(acc[i][j][q], sg[j][q], 0.0f, true, false);
-        const float u0 = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
-        const float g1 = epi_scale_bias(acc[i][j + 1][q], sg[j + 1][q], 0.0f, true, false);
-        const float u1 = epi_scale_bias(acc[i][j + 1 + TO][q], su[j + 1][q], 0.0f, true, false);
-        x[q] = silu_b16(g0) * u0;
-        y[q] = silu_b16(g1) * u1;
-      }
-      const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
-                                                       pack_bf16x2(y[0], y[1]), false, false);
-      const auto w1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[2], x[3]),
-                                                       pack_bf16x2(y[2], y[3]), false, false);
-      const int n = n0 + wn * (WN / 2) + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
-      *(uint4 *)(p.C + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
-    }
-    if constexpr (TO % 2 == 1) {
-      constexpr int j = TO - 1;
-      float h[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma clang fp contract(off)
-        const float g = epi_scale_bias(acc[i][j][q], sg[j][q], 0.0f, true, false);
-        const float u = epi_scale_bias(acc[i][j + TO][q], su[j][q], 0.0f, true, false);
-        h[q] = silu_b16(g) * u;
-      }
-      const int n = n0 + wn * (WN / 2) + j * 16 + 4 * fh;
-      *(uint2 *)(p.C + (size_t)m * p.ldc + n) = make_uint2(pack_bf16x2(h[0], h[1]),
-                                                           pack_bf16x2(h[2], h[3]));
-    }
-  }
-}
-
 // s_waitcnt lgkmcnt(0) as the builtin (vmcnt and expcnt left open): unlike the
 // same text in inline asm, the compiler's wait-count pass sees it, so it does
 // not add a wait of its own for fragments this one already covered (such a
@@ -1264,9 +1205,8 @@ hipError_t launch_linear_w8a8(const int8_t *xq, const float *sx, const int8_t *W
 //    gate/up GEMM runs 256 x 192 or 256 x 256 with 1 x 4 waves of 256 x 48 or
 //    256 x 64, waves 0-1 on the tile's gate rows and waves 2-3 on the up rows
 //    of the same output columns, paired through LDS in the epilogue
-//    (gateup_split_epilogue).  With WMT = 128 (2 x 2 or 1 x 4 waves of 128
-//    rows, the layout these replaced) a gate/up wave pairs its own WN/2 gate
-//    and WN/2 up rows (blocks j and j + TN/2), as gemm_nt_kernel does;
+//    (gateup_split_epilogue).  WMT = 128 (2 x 2 or 1 x 4 waves of 128 rows,
+//    one convert per MFMA) is the plain-GEMM layout these replaced;
 //  * the B fragment reads are inline asm (ds_read8_asm): as C++ reads the
 //    compiler put a full vmcnt(0) before each of them, which took away the
 //    load pipelining and doubled the kernel's time;
@@ -1443,11 +1383,11 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int WM = WMT, WMS = BM / WM, WNS = 4 / WMS;
   constexpr int WN = BN / WNS, TM = WM / 16, TN = WN / 16;
   static_assert(WMT == 128 || (WMT == 256 && BM == 256), "wave tile height");
-  // gate/up with WMT = 256: the tile's B rows are BN/2 gate rows then the BN/2
-  // up rows of the same output columns, so waves 0-1 hold gate sums and waves
-  // 2-3 the up sums of the same columns (paired in the epilogue through LDS);
-  // with WMT = 128 each wave pairs its own blocks j and j + TN/2
-  constexpr bool SPLITGU = GATEUP && WMT == 256;
+  // gate/up (WMT = 256 only): the tile's B rows are BN/2 gate rows then the
+  // BN/2 up rows of the same output columns, so waves 0-1 hold gate sums and
+  // waves 2-3 the up sums of the same columns (paired in the epilogue through
+  // LDS)
+  static_assert(!GATEUP || WMT == 256, "gate/up runs the split layout");
   static_assert(TN >= 2, "the widened-fragment rotation needs two blocks per step");
   // the B widening of a group sits beside its last 8 MFMAs
   constexpr int CU0 = TM - 8;
@@ -1456,7 +1396,6 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int B_DPW = BN / 64;             // 1-KB B loads per wave per stage (16 rows each)
   constexpr int BROW = 64;                   // int8 B row bytes per stage
   static_assert(BM == 256 || BM == 128, "tile height");
-  static_assert(!GATEUP || SPLITGU || TN % 2 == 0, "gate/up pairs blocks j and j + TN/2");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t *As = lds;                                        // [2][BM][64] bf16
   int8_t *Bs = (int8_t *)(lds + 2 * BM * kBK);               // [3][BN][64] int8
@@ -1500,13 +1439,9 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     int n = n0 + r;
     b_up[i] = false;
-    if (SPLITGU) {
+    if (GATEUP) {
       b_up[i] = r >= BN / 2;
       n = n0 + (b_up[i] ? r - BN / 2 : r);
-    } else if (GATEUP) {
-      const int w = r / WN, rr = r % WN;
-      b_up[i] = rr >= WN / 2;
-      n = n0 + w * (WN / 2) + rr % (WN / 2);
     }
     b_kc[i] = c;
     b_off[i] = n < N ? (uint32_t)((size_t)n * p.ldb + c * 16) : kOobOffset;
@@ -1726,15 +1661,9 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   }
   const bool full = m0 + BM <= M && n0 + BN_OUT <= N && (p.ldc & 7) == 0 &&
                     ((uintptr_t)p.C & 15) == 0;
-  if constexpr (SPLITGU) {
+  if constexpr (GATEUP) {
     gateup_split_epilogue<TM, TN, WN>(p, acc, (float *)lds, m0, n0, wn, lane, full);
     return;
-  } else if constexpr (GATEUP) {
-    if (full) {
-      store_gateup_direct<TM, TN, WM, WN>(p, acc, m0, n0, wm, wn, lane);
-      return;
-    }
-    stage_gateup<TM, TN, WM, WN, BN_OUT>(p, acc, lds, n0, wm, wn, lane);
   } else {
     if (full) {
       switch (p.epi) {
