@@ -313,6 +313,7 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    (512, 384, 1040),     # 2-way K split, partial last stage
                                    (384, 1000, 2064),    # 4-way K split, partial N tile
                                    (1000, 1300, 528),    # partial M and N tiles, one K slice
+                                   (256, 256, 16384),    # 8-way K split: one K slice per XCD
                                    # skinny-M MFMA GEMV: partial 16-row tile of
                                    # weights, K % 64 != 0, x rows < 16
                                    (3, 4104, 1040), (16, 1000, 4096),
