@@ -346,19 +346,75 @@ hipError_t launch_quantize_rows_bf16(const uint16_t *x, int64_t M, int64_t K, in
   return hipGetLastError();
 }
 
-// quantize_symmetric_int8 (functional.mojo:231-247), per-tensor scale.
+// quant_legacy from r = 1 / scale (correctly rounded, once) instead of a
+// division per element.  v' = x * r is within two roundings of 2^-24 each of
+// x / scale, so for |v'| < 128 it differs from fl(x / scale) by less than
+// 2^-15: away from the half-integers (where v + 0.5 or v - 0.5 crosses an
+// integer) both give the same t after the +-0.5 add (whose own rounding is at
+// most 2^-17 there) and the same truncation; for |v'| >= 128 both clamp the
+// same way.  Elements within 2^-14 of a half-integer take the division (a
+// uniform branch when any lane of the wave needs it).  NaN -> 0 and an
+// infinite x agree with quant_legacy; a scale whose reciprocal overflows must
+// use quant_legacy (the caller checks r once).
+__device__ __forceinline__ uint32_t quant4_legacy_r(float4 w, float s, float r) {
+  const float x[4] = {w.x, w.y, w.z, w.w};
+  float v[4];
+  bool amb[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+    v[e] = x[e] * r;
+    const float a = fabsf(v[e]);
+    amb[e] = a < 128.0f && fabsf((a - floorf(a)) - 0.5f) < 0x1p-14f;
+  }
+  if (__builtin_amdgcn_ballot_w64(amb[0] | amb[1] | amb[2] | amb[3])) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (amb[e]) v[e] = x[e] / s;
+  }
+  uint32_t out = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    int qe;
+    {
+#pragma clang fp contract(off)
+      const float t = v[e] + (v[e] >= 0.0f ? 0.5f : -0.5f);
+      qe = t != t ? 0 : t >= 127.0f ? 127 : t <= -128.0f ? -128 : (int)t;
+    }
+    out |= (uint32_t)(qe & 0xFF) << (8 * e);
+  }
+  return out;
+}
+
+// quantize_symmetric_int8 (functional.mojo:231-247), per-tensor scale: four
+// elements per thread and step (16-byte loads, 4-byte stores) by the
+// reciprocal rule above, the remainder (and unaligned pointers) one element
+// at a time by quant_legacy.
 __global__ __launch_bounds__(256) void quantize_tensor_legacy(const float *__restrict__ x, int64_t n,
                                                               float scale,
                                                               int8_t *__restrict__ q) {
   const float s = scale == 0.0f ? 1.0f : scale;
+  const float r = 1.0f / s;
+  const bool recip = fabsf(r) < __builtin_inff();
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    q[i] = (int8_t)quant_legacy(x[i], s);
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t done = 0;
+  if ((((uintptr_t)x | (uintptr_t)q) & 15) == 0) {
+    const int64_t n4 = n >> 2;
+    const float4 *x4 = (const float4 *)x;
+    uint32_t *q4 = (uint32_t *)q;
+    for (int64_t c = t0; c < n4; c += stride) {
+      const float4 w = x4[c];
+      q4[c] = recip ? quant4_legacy_r(w, s, r) : quant4(ROUND_LEGACY, w, s, 0.0f);
+    }
+    done = n4 << 2;
+  }
+  for (int64_t i = done + t0; i < n; i += stride) q[i] = (int8_t)quant_legacy(x[i], s);
 }
 
 hipError_t launch_quantize_tensor_legacy(const float *x, int64_t n, float scale, int8_t *q,
                                          hipStream_t stream) {
-  int64_t blocks = (n + 255) / 256;
+  int64_t blocks = (n / 4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(quantize_tensor_legacy, dim3((unsigned)blocks), dim3(256), 0, stream, x, n,

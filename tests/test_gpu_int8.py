@@ -76,6 +76,28 @@ def test_quantize_symmetric_int8_per_tensor(oracle, dev):
         np.testing.assert_array_equal(got, oracle.quantize_symmetric_int8(x, s))
 
 
+@pytest.mark.parametrize("s", [1.0, 0.05, 1.0 / 127, 0.0123])
+def test_quantize_symmetric_int8_ties_and_tails(oracle, dev, s):
+    """The per-tensor quantizer converts four elements per thread from
+    r = 1 / s and takes the division only within 2^-14 of a half-integer
+    quotient: x = (k + 0.5) s and x within 1e-4 s of it must still match the
+    oracle's division bit for bit, on an element count with a tail (not a
+    multiple of 4) and on a view whose start is not 16-byte aligned (the
+    one-element path)."""
+    rng = np.random.default_rng(int(s * 1e4))
+    n = 1_000_003
+    k = rng.integers(-300, 300, n).astype(np.float64) + 0.5
+    x = np.where(rng.random(n) < 0.5, k * s, (k + rng.uniform(-1e-4, 1e-4, n)) * s).astype(np.float32)
+    x[:1000] = (rng.standard_normal(1000) * 3).astype(np.float32)
+    x[1000:1006] = [0.49999997, -0.49999997, 2.5, -2.5, 1e6, -1e6]
+    xs = np.float32(s)
+    got = mj.quantize_symmetric_int8(mj.Tensor(to_dev(x, dev)), float(xs)).numpy()
+    np.testing.assert_array_equal(got, oracle.quantize_symmetric_int8(x, xs))
+    xd = to_dev(x, dev)[1:]  # 4-byte offset: not 16-byte aligned
+    got_u = mj.quantize_symmetric_int8(mj.Tensor(xd), float(xs)).numpy()
+    np.testing.assert_array_equal(got_u, oracle.quantize_symmetric_int8(x[1:], xs))
+
+
 def test_minmax_scale(oracle, dev):
     x = oracle.randn_f32((1000, 37), seed=9)
     x[5, 5] = -7.25
