@@ -6,9 +6,10 @@
 // float, full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), a TB x TB
 // tile per 256-thread workgroup (64; 128 for problems with enough tiles, where
 // each wave then runs 4 x 4 MFMA blocks per LDS fragment read instead of
-// 2 x 2; 32 for tiny latency-bound problems, one block per wave), 16-wide K
-// stages staged through LDS (k-major, padded).  The tile
-// size does not change any output's summation order.  Operands come as (pointer, row stride, column stride), which
+// 2 x 2; 32 for tiny latency-bound problems, one block per wave), K stages
+// staged through LDS (k-major, padded; 16 deep, 64 (fp32) or 32 (fp64) on the
+// 32 x 32 tiles).  Neither the tile size nor the stage depth changes any
+// output's summation order.  Operands come as (pointer, row stride, column stride), which
 // covers the reference's zero-copy transpose views; the loader walks
 // whichever dimension has unit stride with consecutive lanes so global reads
 // stay coalesced.  A grid dimension over broadcast batch indices serves
@@ -46,7 +47,7 @@ template <> struct Acc<double> {
 // value plus the finished product, one rounding).
 // The batch index (batch0 + blockIdx.y) is decomposed over up to 5 broadcast
 // batch dimensions into element offsets of A and B; C is contiguous per batch.
-template <typename T, int TB>
+template <typename T, int TB, int BK = kFBK>
 __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const T *__restrict__ A,
                                                       int64_t sAm, int64_t sAk,
                                                       const T *__restrict__ B, int64_t sBk,
@@ -54,11 +55,13 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
                                                       int epi, int accum, T *__restrict__ C,
                                                       int64_t ldc, BatchDesc bd, int64_t batch0) {
   constexpr int kFBM = TB, kFBN = TB;
-  constexpr int NB = TB / 32;   // 16 x 16 blocks per wave and dimension (waves 2 x 2)
-  constexpr int EPT = TB / 16;  // elements of each operand per thread per stage
-  constexpr int MF = 256 / TB;  // m-fast / n-fast loader: k rows per pass
-  __shared__ T As[2][kFBK][kFBM + 4];
-  __shared__ T Bs[2][kFBK][kFBN + 4];
+  constexpr int NB = TB / 32;        // 16 x 16 blocks per wave and dimension (waves 2 x 2)
+  constexpr int EPT = TB * BK / 256; // elements of each operand per thread per stage
+  constexpr int MF = 256 / TB;       // m-fast / n-fast loader: k rows per pass
+  constexpr int KF = 256 / BK;       // k-fast loader: m (n) columns per pass
+  static_assert(EPT >= 1 && BK % 4 == 0, "stage shape");
+  __shared__ T As[2][BK][kFBM + 4];
+  __shared__ T Bs[2][BK][kFBN + 4];
 
   {
     const int64_t bi = batch0 + blockIdx.y;
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       int m, k;
-      if (a_k_fast) { k = tid & 15; m = (tid >> 4) + 16 * i; }
+      if (a_k_fast) { k = tid % BK; m = tid / BK + KF * i; }
       else          { m = tid % TB; k = tid / TB + MF * i; }
       const int gm = m0 + m, gk = k0 + k;
       ra[i] = (gm < M && gk < K) ? A[(int64_t)gm * sAm + (int64_t)gk * sAk] : T(0);
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
     for (int i = 0; i < EPT; ++i) {
       int n, k;
       if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
-      else          { k = tid & 15; n = (tid >> 4) + 16 * i; }
+      else          { k = tid % BK; n = tid / BK + KF * i; }
       const int gn = n0 + n, gk = k0 + k;
       rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : T(0);
     }
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       int m, k;
-      if (a_k_fast) { k = tid & 15; m = (tid >> 4) + 16 * i; }
+      if (a_k_fast) { k = tid % BK; m = tid / BK + KF * i; }
       else          { m = tid % TB; k = tid / TB + MF * i; }
       As[buf][k][m] = ra[i];
     }
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
     for (int i = 0; i < EPT; ++i) {
       int n, k;
       if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
-      else          { k = tid & 15; n = (tid >> 4) + 16 * i; }
+      else          { k = tid % BK; n = tid / BK + KF * i; }
       Bs[buf][k][n] = rb[i];
     }
   };
@@ -129,16 +132,16 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = T(0);
 
-  const int nk = (K + kFBK - 1) / kFBK;
+  const int nk = (K + BK - 1) / BK;
   load(0);
   store(0);
   __syncthreads();
   const int fr = lane & 15, fk = lane >> 4;
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) load((kt + 1) * kFBK);
+    if (kt + 1 < nk) load((kt + 1) * BK);
 #pragma unroll
-    for (int kk = 0; kk < kFBK; kk += 4) {
+    for (int kk = 0; kk < BK; kk += 4) {
       T a[NB], b[NB];
 #pragma unroll
       for (int i = 0; i < NB; ++i) a[i] = As[buf][kk + fk][wm * (TB / 2) + i * 16 + fr];
@@ -181,6 +184,13 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   }
 }
 
+// K per stage of the 32 x 32 tiles: each stage costs a global-load round
+// trip that its MFMAs (BK / 4 per wave) cannot cover, so the latency-bound
+// tiny problems take deep stages (fp32: 64, 37 KB of LDS; fp64: 32, the
+// static LDS limit); per output the k order is the same at any depth
+template <typename T>
+constexpr int kTinyBK = sizeof(T) == 4 ? 64 : 32;
+
 template <typename T>
 static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t sAm,
                             int64_t sAk, const T *B, int64_t sBk, int64_t sBn, const T *bias,
@@ -206,7 +216,7 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
                          ldc, bd, b0);
     else if (tiny)
-      hipLaunchKernelGGL((gemm_fx_kernel<T, 32>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 32, kTinyBK<T>>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
                          ldc, bd, b0);
     else

@@ -67,6 +67,21 @@ def test_matmul_large_tiles_integer_exact(oracle, dev, ta, tb):
     np.testing.assert_array_equal(got, oracle.matmul_f32(A, B))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(100, 90, 200), (31, 33, 130), (256, 256, 256)])
+def test_matmul_small_tiles_integer_exact(oracle, dev, dtype, ta, tb, M, N, K):
+    """Problems of fewer than 64 tiles of 64 x 64 run on 32 x 32 tiles with
+    deep K stages (64 for fp32, 32 for fp64); K here is not a multiple of
+    the stage, so the last stage is zero-filled, and the transposed views
+    take the k-fast loaders.  Small-integer operands make every sum exact."""
+    rng = np.random.default_rng(M + 3 * N + K + 2 * ta + tb)
+    A = rng.integers(-8, 9, size=(M, K)).astype(dtype)
+    B = rng.integers(-8, 9, size=(K, N)).astype(dtype)
+    got = mj.matmul(_view(A, dev, ta), _view(B, dev, tb)).numpy()
+    np.testing.assert_array_equal(got, (A.astype(np.float64) @ B.astype(np.float64)).astype(dtype))
+
+
 def test_matmul_transposed_views(oracle, dev):
     """x.matmul(W.transpose()) and A.transpose().matmul(B) run on the stride
     views, as the reference's strided path does (broadcast.mojo:1647-1673)."""
