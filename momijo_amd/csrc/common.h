@@ -163,10 +163,14 @@ __device__ __forceinline__ float apply_epi(int epi, float v) {
 // a quarter of the VALU cycles of the expf + IEEE division forms, which a
 // GEMM epilogue spends with nothing left to overlap (C4: 128 GELUs per lane,
 // 16 us of a 71 us launch before this form).
+// The exponent -2 k log2(e) (x + 0.044715 x^3) is evaluated as x (a + a c x^2)
+// (one multiply fewer than the literal nesting; the two differ by an ulp or
+// two of the exponent, inside the error stated above).
 __device__ __forceinline__ float gelu_b16(float x) {
-  const float a = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 k log2(e)
-  const float u = x + 0.044715f * (x * x * x);
-  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * u));
+  constexpr float a = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634);  // -2 k log2(e)
+  constexpr float ac = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634 * 0.044715);
+  const float z = x * __builtin_fmaf(x * x, ac, a);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 __device__ __forceinline__ float silu_b16(float x) {
