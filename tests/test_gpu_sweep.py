@@ -1,0 +1,136 @@
+"""Seeded shape sweeps of the GEMM planners against the oracle, bit for bit.
+
+Each family draws its shapes from a fixed seed, spread over the ranges where
+the planners switch kernels: M from 1 (GEMVs) through the skinny-M GEMV
+(M <= 16) to multi-tile GEMMs, N and K ragged against every tile, stage and
+K-split boundary, with and without bias.  The operands make every sum exact
+(small integers, power-of-two scales) or the path is exact by construction
+(int8 sums, W8A8's integer GEMM and fixed epilogue order), so whichever tile,
+split or pipeline the planner picks, the output must equal the oracle's.
+Problem sizes are capped so the oracle's scalar loops stay at a fraction of a
+second per case.
+"""
+import numpy as np
+import pytest
+
+import momijo_amd as mj
+from _util import bf16_dev, bf16_host_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+_MAC_CAP = 2.0e8
+
+
+def _draw_m(rng):
+    """M spread over the GEMV, skinny-GEMV and tile ranges."""
+    band = rng.integers(0, 4)
+    if band == 0:
+        return 1
+    if band == 1:
+        return int(rng.integers(2, 17))
+    if band == 2:
+        return int(rng.integers(17, 300))
+    return int(rng.integers(300, 2200))
+
+
+def _cap(M, N, K, step, n_first):
+    """Shrink N, then K (kept a multiple of step), or K first, until
+    M * N * K fits the cap; shrinking N first keeps long K loops (and the
+    K splits of few-tile problems) in the sweep."""
+    def shrink_n(N, K):
+        while M * N * K > _MAC_CAP and N > 16:
+            N = max(16, N // 2)
+        return N, K
+
+    def shrink_k(N, K):
+        while M * N * K > _MAC_CAP and K > step:
+            K = max(step, (K // 2) // step * step)
+        return N, K
+
+    N, K = shrink_n(*shrink_k(N, K)) if not n_first else shrink_k(*shrink_n(N, K))
+    while M * N * K > _MAC_CAP and N > 1:
+        N = max(1, N // 2)
+    return N, K
+
+
+def _shapes(seed, count, kstep, kmax, nmax):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        M = _draw_m(rng)
+        N = int(rng.integers(1, nmax + 1))
+        K = int(rng.integers(1, kmax // kstep + 1)) * kstep
+        N, K = _cap(M, N, K, kstep, bool(rng.integers(0, 2)))
+        out.append((M, N, K, bool(rng.integers(0, 2)), int(rng.integers(0, 2))))
+    return out
+
+
+_W8A16 = _shapes(101, 48, 16, 8192, 6000)
+_BF16 = _shapes(202, 32, 8, 4096, 3000)
+_I8 = _shapes(303, 24, 1, 3000, 2500)
+_W8A8 = _shapes(404, 24, 16, 6144, 3000)
+
+
+def _epi(flag):
+    return mj.EPI_RELU if flag else mj.EPI_NONE
+
+
+@pytest.mark.parametrize("M,N,K,with_bias,relu", _W8A16)
+def test_sweep_w8a16_linear(oracle, dev, M, N, K, with_bias, relu):
+    """Integer activations in [-2, 2], int8 weights, scales 2^-8 .. 2^-3 and
+    biases in quarter steps: |sum| <= 254 K < 2^21, so the sums, the scaled
+    sums and the biased results are exact in fp32 and the bf16 rounding is
+    the only one."""
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    x = oracle.f32_to_bf16(rng.integers(-2, 3, size=(M, K)).astype(np.float32))
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, size=N)).astype(np.float32)
+    b = (rng.integers(-8, 9, size=N).astype(np.float32) / np.float32(4)) if with_bias else None
+    lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), None if b is None else to_dev(b, dev),
+                      _epi(relu))
+    got = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
+    ref, _ = oracle.linear_w8a16(x, Q, s, b, _epi(relu))
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,N,K,with_bias,relu", _BF16)
+def test_sweep_bf16_gemm(oracle, dev, M, N, K, with_bias, relu):
+    """bf16 A [M, K] . B [N, K]^T with integer operands in [-4, 4] and biases
+    in quarter steps: the sums are exact (|sum| <= 16 K), so the bf16 outputs
+    must match on every tile and pipeline the planner picks."""
+    rng = np.random.default_rng(M * 5 + N * 11 + K)
+    A = oracle.f32_to_bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
+    B = oracle.f32_to_bf16(rng.integers(-4, 5, size=(N, K)).astype(np.float32))
+    b = (rng.integers(-8, 9, size=N).astype(np.float32) / np.float32(4)) if with_bias else None
+    C = mj.gemm_bf16_nt(bf16_dev(A, dev), bf16_dev(B, dev), None if b is None else to_dev(b, dev),
+                        _epi(relu))
+    ref, _ = oracle.gemm_bf16_nt(A, B, b, _epi(relu))
+    np.testing.assert_array_equal(bf16_host_bits(C), ref)
+
+
+@pytest.mark.parametrize("M,N,K,_b,_r", _I8)
+def test_sweep_int8_gemm(oracle, dev, M, N, K, _b, _r):
+    """matmul_i8_i8_to_i32 at any K (K % 16 != 0 takes the generic kernel):
+    int32 sums are exact, so bit-exact on every shape."""
+    rng = np.random.default_rng(M * 13 + N + K * 3)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+    got = mj.matmul_i8_i8_to_i32(mj.Tensor(to_dev(A, dev)), mj.Tensor(to_dev(B, dev)).transpose())
+    np.testing.assert_array_equal(got.numpy(), oracle.matmul_i8_i8_to_i32(A, B))
+
+
+@pytest.mark.parametrize("M,N,K,with_bias,relu", _W8A8)
+def test_sweep_w8a8_linear(oracle, dev, M, N, K, with_bias, relu):
+    """W8A8 with dynamic per-row activation scales: the row quantize and the
+    int32 sums are exact and the epilogue's fp32 operations are those of the
+    oracle in the same order, so the bf16 outputs match bit for bit."""
+    rng = np.random.default_rng(M * 3 + N * 17 + K)
+    x = oracle.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = oracle.randu_f32((N,), 0.0005, 0.004, seed=M + N + K)
+    b = oracle.randu_f32((N,), -0.25, 0.25, seed=M + N + K + 1) if with_bias else None
+    lin = mj.W8A8Linear(to_dev(Q, dev), to_dev(sw, dev), None if b is None else to_dev(b, dev),
+                        _epi(relu))
+    got = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
+    ref, _, _, _ = oracle.linear_w8a8(x, Q, sw, b, _epi(relu))
+    np.testing.assert_array_equal(got, ref)
