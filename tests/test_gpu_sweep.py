@@ -7,14 +7,15 @@ K-split boundary, with and without bias.  The operands make every sum exact
 (small integers, power-of-two scales) or the path is exact by construction
 (int8 sums, W8A8's integer GEMM and fixed epilogue order), so whichever tile,
 split or pipeline the planner picks, the output must equal the oracle's.
-Problem sizes are capped so the oracle's scalar loops stay at a fraction of a
+The FFN family is checked to the bf16 bar (its SiLU is not exact).  Problem
+sizes are capped so the oracle's scalar loops stay at a fraction of a
 second per case.
 """
 import numpy as np
 import pytest
 
 import momijo_amd as mj
-from _util import bf16_dev, bf16_host_bits, to_dev
+from _util import bf16_dev, bf16_host_bits, bf16_host_f32, normwise_rel, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -69,6 +70,37 @@ _W8A16 = _shapes(101, 48, 16, 8192, 6000)
 _BF16 = _shapes(202, 32, 8, 4096, 3000)
 _I8 = _shapes(303, 24, 1, 3000, 2500)
 _W8A8 = _shapes(404, 24, 16, 6144, 3000)
+
+
+def _mlp_shapes(seed, count):
+    """(M, K, I, H) with K, I multiples of 16 and M (2 I K + H I) capped."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        M = _draw_m(rng)
+        K = int(rng.integers(1, 257)) * 16
+        I = int(rng.integers(1, 257)) * 16
+        H = int(rng.integers(1, 3001))
+        while M * (2 * I * K + H * I) > _MAC_CAP and max(K, I) > 16:
+            if K >= I:
+                K = max(16, (K // 2) // 16 * 16)
+            else:
+                I = max(16, (I // 2) // 16 * 16)
+        while M * (2 * I * K + H * I) > _MAC_CAP and H > 1:
+            H = max(1, H // 2)
+        out.append((M, K, I, H))
+    return out
+
+
+def _f32_shapes(seed, count):
+    """(M, N, K, transpose A, transpose B) for the fp32 engine."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 700)), int(rng.integers(1, 700)), int(rng.integers(1, 700)),
+             bool(rng.integers(0, 2)), bool(rng.integers(0, 2))) for _ in range(count)]
+
+
+_MLP = _mlp_shapes(505, 16)
+_F32 = _f32_shapes(606, 24)
 
 
 def _epi(flag):
@@ -134,3 +166,38 @@ def test_sweep_w8a8_linear(oracle, dev, M, N, K, with_bias, relu):
     got = bf16_host_bits(lin.forward(bf16_dev(x, dev)))
     ref, _, _, _ = oracle.linear_w8a8(x, Q, sw, b, _epi(relu))
     np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,K,I,H", _MLP)
+def test_sweep_w8a16_mlp(oracle, dev, M, K, I, H):
+    """The SiLU-gated FFN (gate/up GEMM or GEMV, SiLU * up, down projection
+    with or without a K split) against the oracle's FFN within the bf16
+    bar (normwise 2e-2 on h and on y); a wrong tile, split or column
+    pairing moves whole blocks by their own magnitude."""
+    x = oracle.f32_to_bf16(oracle.randn_f32((M, K), seed=M + K))
+    Wg, sg = oracle.quantize_rowwise_rhe(oracle.randn_f32((I, K), std=0.02, seed=I + 1))
+    Wu, su = oracle.quantize_rowwise_rhe(oracle.randn_f32((I, K), std=0.02, seed=I + 2))
+    Wd, sd = oracle.quantize_rowwise_rhe(oracle.randn_f32((H, I), std=0.02, seed=H + 3))
+    mk = lambda q, s: mj.W8Linear(to_dev(q, dev), to_dev(s, dev))  # noqa: E731
+    y, h = mj.W8MLP(mk(Wg, sg), mk(Wu, su), mk(Wd, sd)).forward(bf16_dev(x, dev))
+    hr, yr = oracle.mlp_w8a16(x, Wg, sg, Wu, su, Wd, sd)
+    assert normwise_rel(bf16_host_f32(h), oracle.bf16_to_f32(hr)) <= 2e-2
+    assert normwise_rel(bf16_host_f32(y), oracle.bf16_to_f32(yr)) <= 2e-2
+
+
+def _f32_view(M, dev, transposed):
+    if not transposed:
+        return mj.Tensor(to_dev(M, dev))
+    return mj.Tensor(to_dev(np.ascontiguousarray(M.T), dev)).transpose()
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _F32)
+def test_sweep_f32_matmul(dev, M, N, K, ta, tb):
+    """fp32 matmul on the MFMA engine over every tile size (32, 64, 128) and
+    loader orientation: small-integer operands make the sums exact, so the
+    result equals the exact product."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A = rng.integers(-8, 9, size=(M, K)).astype(np.float32)
+    B = rng.integers(-8, 9, size=(K, N)).astype(np.float32)
+    got = mj.matmul(_f32_view(A, dev, ta), _f32_view(B, dev, tb)).numpy()
+    np.testing.assert_array_equal(got, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
