@@ -11,6 +11,9 @@ The FFN family is checked to the bf16 bar (its SiLU is not exact).  Problem
 sizes are capped so the oracle's scalar loops stay at a fraction of a
 second per case.
 """
+import os
+import time
+
 import numpy as np
 import pytest
 
@@ -201,3 +204,87 @@ def test_sweep_f32_matmul(dev, M, N, K, ta, tb):
     B = rng.integers(-8, 9, size=(K, N)).astype(np.float32)
     got = mj.matmul(_f32_view(A, dev, ta), _f32_view(B, dev, tb)).numpy()
     np.testing.assert_array_equal(got, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
+# ------------------------------------------------------------- long sweep
+# Opt-in (MJ_LONG_SWEEP=<seconds>): random shapes up to M = 4096, N = 12000,
+# K = 16384 for as long as asked, over the W8A16 Linear, the bf16 GEMM, the
+# int8 GEMM and the fp32 matmul (with transposed views), every output compared
+# with exact float64 products (small-integer operands, power-of-two scales)
+# rounded by the oracle's pinned bf16 rounding.
+_LONG = float(os.environ.get("MJ_LONG_SWEEP", "0"))
+
+
+def _long_case(rng, fam, dev, to_bf16):
+    def draw_m():
+        return [1, int(rng.integers(2, 17)), int(rng.integers(17, 257)),
+                int(rng.integers(257, 1500)), int(rng.integers(1500, 4097))][rng.integers(0, 5)]
+
+    def cap(M, N, K, step):
+        while M * N * K > 3e10 and (N > 16 or K > step):
+            if (rng.integers(0, 2) and K > step) or N <= 16:
+                K = max(step, (K // 2) // step * step)
+            else:
+                N = max(16, N // 2)
+        return N, K
+
+    def bf16_ref(sum64, s, b, relu):
+        v = sum64 * (1.0 if s is None else s[None, :]) + (0.0 if b is None else b[None, :])
+        v = v.astype(np.float32)
+        return to_bf16(np.where(v > 0, v, np.float32(0)) if relu else v)
+
+    relu = bool(rng.integers(0, 2))
+    epi = mj.EPI_RELU if relu else mj.EPI_NONE
+    if fam == "w8a16":
+        M, N, K = draw_m(), int(rng.integers(1, 12001)), int(rng.integers(1, 1025)) * 16
+        N, K = cap(M, N, K, 16)
+        x = rng.integers(-2, 3, size=(M, K)).astype(np.float32)
+        Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+        s = (2.0 ** rng.integers(-8, -2, size=N)).astype(np.float32)
+        b = (rng.integers(-8, 9, size=N) / 4).astype(np.float32) if rng.integers(0, 2) else None
+        lin = mj.W8Linear(to_dev(Q, dev), to_dev(s, dev), None if b is None else to_dev(b, dev), epi)
+        got = bf16_host_bits(lin.forward(bf16_dev(to_bf16(x), dev)))
+        ref = bf16_ref(x.astype(np.float64) @ Q.astype(np.float64).T, s.astype(np.float64),
+                       None if b is None else b.astype(np.float64), relu)
+    elif fam == "bf16":
+        M, N, K = draw_m(), int(rng.integers(1, 9001)), int(rng.integers(1, 1025)) * 8
+        N, K = cap(M, N, K, 8)
+        A = rng.integers(-4, 5, size=(M, K)).astype(np.float32)
+        B = rng.integers(-4, 5, size=(N, K)).astype(np.float32)
+        b = (rng.integers(-8, 9, size=N) / 4).astype(np.float32) if rng.integers(0, 2) else None
+        got = bf16_host_bits(mj.gemm_bf16_nt(bf16_dev(to_bf16(A), dev),
+                                             bf16_dev(to_bf16(B), dev),
+                                             None if b is None else to_dev(b, dev), epi))
+        ref = bf16_ref(A.astype(np.float64) @ B.astype(np.float64).T, None,
+                       None if b is None else b.astype(np.float64), relu)
+    elif fam == "i8":
+        M, N, K = draw_m(), int(rng.integers(1, 9001)), int(rng.integers(1, 8193))
+        N, K = cap(M, N, K, 1)
+        A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+        got = mj.matmul_i8_i8_to_i32(mj.Tensor(to_dev(A, dev)), mj.Tensor(to_dev(B, dev)).transpose()).numpy()
+        ref = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int32)
+    else:
+        M, N, K = (int(v) for v in rng.integers(1, 3000, size=3))
+        ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        A = rng.integers(-8, 9, size=(M, K)).astype(np.float32)
+        B = rng.integers(-8, 9, size=(K, N)).astype(np.float32)
+        got = mj.matmul(_f32_view(A, dev, ta), _f32_view(B, dev, tb)).numpy()
+        ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    return (fam, M, N, K), got, ref
+
+
+@pytest.mark.skipif(_LONG <= 0, reason="opt-in: set MJ_LONG_SWEEP=<seconds>")
+def test_long_random_sweep(oracle, dev):
+    rng = np.random.default_rng(int(os.environ.get("MJ_LONG_SWEEP_SEED", "7")))
+    t_end, n, bad = time.time() + _LONG, 0, []
+    fams = ("w8a16", "bf16", "i8", "f32")
+    while time.time() < t_end:
+        desc, got, ref = _long_case(rng, fams[n % 4], dev, oracle.f32_to_bf16)
+        n += 1
+        if got.shape != ref.shape or not np.array_equal(got, ref):
+            bad.append(desc)
+        if n % 50 == 0:
+            print(f"{n} cases, {len(bad)} mismatches (last {desc})", flush=True)
+    print(f"{n} cases, {len(bad)} mismatches", flush=True)
+    assert not bad, bad[:10]
