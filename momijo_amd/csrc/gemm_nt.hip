@@ -1922,7 +1922,8 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
                        p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
   if (p.gate_up) {
-    // output columns per tile are BN/2 = 128; only BN = 256 pairs gate and up.
+    // output columns per tile are BN/2: 128 at BN = 256 (the 8-wave kernel
+    // for M <= 128 takes only that), 96 at BN = 192 on the tile kernel below.
     // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
     // and up: 20 us faster than the 8-wave kernel) in its split layout: 1 x 4
     // waves of 256 x BN/4, gate rows in waves 0-1 and the up rows of the same

@@ -129,7 +129,7 @@ def test_bf16_gelu_silu_epilogue_exact_sums(oracle, dev, M, N, epi):
     literal expf/division forms: every output within one bf16 step (2^-7
     relative) of the oracle's fp32 value or 1e-6 absolute, and at most 1 % of
     the bits differing outside GELU's cancelling range x < -2.  4096 x 4096
-    runs the 256 x 256 one-wave-per-SIMD kernel (direct stores), 300 x 200
+    runs the 256 x 256 two-waves-per-SIMD kernel (direct stores), 300 x 200
     edge tiles through the staged epilogue."""
     K = 16
     rng = np.random.default_rng(M + N + epi)
