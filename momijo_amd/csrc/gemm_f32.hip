@@ -9,7 +9,8 @@
 // 2 x 2; 32 for tiny latency-bound problems, one block per wave), K stages
 // staged through LDS (k-major, padded; 16 deep, 64 (fp32) or 32 (fp64) on the
 // 32 x 32 tiles).  Neither the tile size nor the stage depth changes any
-// output's summation order.  Operands come as (pointer, row stride, column stride), which
+// output's summation order.  Tiny fp32 products whose operands are both
+// k-contiguous skip LDS (gemm_f32_direct_kernel, same MFMA sequence).  Operands come as (pointer, row stride, column stride), which
 // covers the reference's zero-copy transpose views; the loader walks
 // whichever dimension has unit stride with consecutive lanes so global reads
 // stay coalesced.  A grid dimension over broadcast batch indices serves
@@ -184,6 +185,93 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   }
 }
 
+// 16 x 16 outputs per 64-thread workgroup for tiny fp32 products whose
+// operands are both k-contiguous (x . W^T: the Linear forward, and matmul
+// with a transposed right operand), without LDS: lane l = fr + 16 j loads
+// A[fr][16 u + 4 j .. + 3] and B^T[fr][16 u + 4 j .. + 3] of each 16-deep
+// chunk u as one 16-byte load, and a 4 x 4 transpose across the four 16-lane
+// rows (two v_permlane32_swap, then two v_permlane16_swap) leaves in register
+// c of lane fr + 16 j the element k = 16 u + 4 c + j, the operand that the
+// MFMA t = 4 u + c takes from that lane.  So the outputs see the MFMA
+// sequence of gemm_fx_kernel in the same k order, bit for bit (chunks past K
+// are zero, as the staged kernel's padding is).  Loads run two batches of CB
+// chunks ahead of the MFMAs; needs K % 4 == 0 and 16-byte aligned rows.
+__device__ __forceinline__ void transpose4_rows(f32x4 &v) {
+  const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]),
+                                                   false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]),
+                                                   false, false);
+  const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+  const auto t1 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+  v = f32x4{__uint_as_float(t0[0]), __uint_as_float(t0[1]), __uint_as_float(t1[0]),
+            __uint_as_float(t1[1])};
+}
+
+template <int CB>
+__global__ __launch_bounds__(64) void gemm_f32_direct_kernel(int M, int N, int K,
+                                                             const float *__restrict__ A,
+                                                             int64_t sAm,
+                                                             const float *__restrict__ Bt,
+                                                             int64_t sBn,
+                                                             const float *__restrict__ bias,
+                                                             int epi, float *__restrict__ C,
+                                                             int64_t ldc) {
+  const int lane = threadIdx.x;
+  const int fr = lane & 15, j = lane >> 4;
+  const int tiles_n = (N + 15) / 16;
+  const int m0 = (blockIdx.x / tiles_n) * 16, n0 = (blockIdx.x % tiles_n) * 16;
+  const bool am = m0 + fr < M, bn = n0 + fr < N;
+  const float *pa = A + (am ? (int64_t)(m0 + fr) * sAm : 0) + 4 * j;
+  const float *pb = Bt + (bn ? (int64_t)(n0 + fr) * sBn : 0) + 4 * j;
+  const int nc = (K + 15) / 16;
+  f32x4 xa[CB], xb[CB], ya[CB], yb[CB];
+  auto load = [&](f32x4 (&ra)[CB], f32x4 (&rb)[CB], int c0) {
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      const bool ok = (c0 + c) * 16 + 4 * j < K;  // K % 4 == 0: wholly in or out
+      ra[c] = am && ok ? *(const f32x4 *)(pa + (int64_t)(c0 + c) * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
+      rb[c] = bn && ok ? *(const f32x4 *)(pb + (int64_t)(c0 + c) * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](f32x4 (&ra)[CB], f32x4 (&rb)[CB], int c0) {
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      if (c0 + c >= nc) break;
+      transpose4_rows(ra[c]);
+      transpose4_rows(rb[c]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[c][q], rb[c][q], acc, 0, 0, 0);
+    }
+  };
+  load(xa, xb, 0);
+  for (int c0 = 0;;) {
+    if (c0 + CB < nc) load(ya, yb, c0 + CB);
+    compute(xa, xb, c0);
+    c0 += CB;
+    if (c0 >= nc) break;
+    if (c0 + CB < nc) load(xa, xb, c0 + CB);
+    compute(ya, yb, c0);
+    c0 += CB;
+    if (c0 >= nc) break;
+  }
+  const int n = n0 + fr;
+  if (!bn) return;
+  const float bb = bias ? bias[n] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = m0 + Acc<float>::row(lane, r);
+    if (m < M) {
+      float v = acc[r];
+      if (bias) {
+#pragma clang fp contract(off)
+        v = v + bb;
+      }
+      C[(int64_t)m * ldc + n] = apply_epi(epi, v);
+    }
+  }
+}
+
 // K per stage of the 32 x 32 tiles: each stage costs a global-load round
 // trip that its MFMAs (BK / 4 per wave) cannot cover, so the latency-bound
 // tiny problems take deep stages (fp32: 64, 37 KB of LDS; fp64: 32, the
@@ -204,6 +292,17 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool big = M >= 256 && N >= 256 && tiles128 * batches >= 512;
   const bool tiny = !big && ((M + 63) / 64) * ((N + 63) / 64) * batches < 64;
+  if constexpr (sizeof(T) == sizeof(float)) {
+    const bool direct = tiny && batches == 1 && bd.rank == 0 && !accum && sAk == 1 && sBk == 1 &&
+                        K % 4 == 0 && (M == 1 || sAm % 4 == 0) && (N == 1 || sBn % 4 == 0) &&
+                        (((uintptr_t)A | (uintptr_t)B) & 15) == 0;
+    if (direct) {
+      const int64_t tiles16 = ((M + 15) / 16) * ((N + 15) / 16);
+      hipLaunchKernelGGL(gemm_f32_direct_kernel<8>, dim3((unsigned)tiles16), dim3(64), 0, stream,
+                         (int)M, (int)N, (int)K, A, sAm, B, sBn, bias, epi, C, ldc);
+      return hipGetLastError();
+    }
+  }
   const int TBs = big ? 128 : (tiny ? 32 : 64);
   const int64_t tiles64 = ((M + TBs - 1) / TBs) * ((N + TBs - 1) / TBs);
   if (tiles64 > INT32_MAX) return hipErrorInvalidValue;  // grid.x limit

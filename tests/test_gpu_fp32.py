@@ -82,6 +82,27 @@ def test_matmul_small_tiles_integer_exact(oracle, dev, dtype, ta, tb, M, N, K):
     np.testing.assert_array_equal(got, (A.astype(np.float64) @ B.astype(np.float64)).astype(dtype))
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (100, 90, 200), (1, 300, 64), (37, 1000, 252),
+                                   (37, 1000, 1004), (250, 3, 4096), (16, 16, 4)])
+def test_direct_and_staged_small_tiles_agree_bitwise(oracle, dev, M, N, K):
+    """The same product of N(0,1) operands through both fp32 small-problem
+    kernels: with B as the transpose of a contiguous [N, K] (k-contiguous
+    rows, the LDS-free kernel) and as a contiguous [K, N] (the staged 32 x 32
+    kernel).  Both issue the same MFMA sequence in the same k order, so the
+    results are identical bit for bit, not just within the fp32 bar (checked
+    against the oracle up to K = 256: at K ~ 1000 and beyond, outputs that
+    cancel to near zero differ from the strict-order sum by more than 1e-5
+    absolute in either kernel)."""
+    A = oracle.randn_f32((M, K), seed=M + K)
+    B = oracle.randn_f32((K, N), seed=N + 2 * K)
+    a = mj.Tensor(to_dev(A, dev))
+    direct = mj.matmul(a, mj.Tensor(to_dev(np.ascontiguousarray(B.T), dev)).transpose()).numpy()
+    staged = mj.matmul(a, mj.Tensor(to_dev(B, dev))).numpy()
+    np.testing.assert_array_equal(direct, staged)
+    if K <= 256:
+        assert_close_f32(direct, oracle.matmul_f32(A, B))
+
+
 def test_matmul_transposed_views(oracle, dev):
     """x.matmul(W.transpose()) and A.transpose().matmul(B) run on the stride
     views, as the reference's strided path does (broadcast.mojo:1647-1673)."""
