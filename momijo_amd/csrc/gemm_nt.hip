@@ -1699,8 +1699,10 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
 // activation and the bf16 rounding.  Rows of a multiple of 8 columns with a
 // 16-byte aligned output, scales and bias take 8 columns per thread: the
 // thread's scales and biases and all of its partial loads (two 16-byte
-// nontemporal loads per split) are issued before the sums, and the result is
-// one 16-byte store; anything else takes 4 columns per thread.
+// loads per split) are issued before the sums, and the result is one 16-byte
+// store; anything else takes 4 columns per thread.  The partials were written
+// by the GEMM just before: plain loads read them 6 % faster than nontemporal
+// ones (C5's down projection, 8.33 -> 7.86 us on MI355X).
 template <int E>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
   const int M = (int)p.M, N = (int)p.N;
@@ -1733,8 +1735,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmNT p) {
 #pragma unroll
       for (int sp = 0; sp < 8; ++sp) {
         if (sp < p.splits) {
-          part[sp][0] = __builtin_nontemporal_load((const f32x4 *)(src + sp * plane));
-          part[sp][1] = __builtin_nontemporal_load((const f32x4 *)(src + sp * plane + 4));
+          part[sp][0] = *(const f32x4 *)(src + sp * plane);
+          part[sp][1] = *(const f32x4 *)(src + sp * plane + 4);
         }
       }
       float v[8];
