@@ -211,11 +211,13 @@ def test_sweep_f32_matmul(dev, M, N, K, ta, tb):
 # K = 16384 for as long as asked, over the W8A16 Linear, the bf16 GEMM, the
 # int8 GEMM and the fp32 matmul (with transposed views), every output compared
 # with exact float64 products (small-integer operands, power-of-two scales)
-# rounded by the oracle's pinned bf16 rounding.
+# rounded by the oracle's pinned bf16 rounding; and over the two quantizers
+# (per-row RHE / legacy with exact-tie rows, per-tensor legacy with
+# near-ties), bit for bit against the oracle.
 _LONG = float(os.environ.get("MJ_LONG_SWEEP", "0"))
 
 
-def _long_case(rng, fam, dev, to_bf16):
+def _long_case(rng, fam, dev, to_bf16, oracle_quantize_rowwise=None, oracle_quantize_tensor=None):
     def draw_m():
         return [1, int(rng.integers(2, 17)), int(rng.integers(17, 257)),
                 int(rng.integers(257, 1500)), int(rng.integers(1500, 4097))][rng.integers(0, 5)]
@@ -264,6 +266,33 @@ def _long_case(rng, fam, dev, to_bf16):
         B = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
         got = mj.matmul_i8_i8_to_i32(mj.Tensor(to_dev(A, dev)), mj.Tensor(to_dev(B, dev)).transpose()).numpy()
         ref = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int32)
+    elif fam == "qrow":
+        # per-row quantize/pack: random rows over many decades, rows of exact
+        # ties (absmax 127 * 2^e, others (k + 1/2) 2^e), all-zero rows
+        N, K = int(rng.integers(1, 3001)), int(rng.integers(1, 9001))
+        W = (rng.standard_normal((N, K)) * 10.0 ** rng.uniform(-6, 6, size=(N, 1))).astype(np.float32)
+        kind = rng.integers(0, 8, size=N)
+        e = rng.integers(-20, 20, size=N).astype(np.float64)
+        ties = (rng.integers(-127, 127, size=(N, K)) + 0.5) * 2.0 ** e[:, None]
+        ties[:, 0] = 127 * 2.0 ** e
+        W = np.where((kind == 0)[:, None], ties.astype(np.float32), W)
+        W[kind == 1] = 0.0
+        rounding = mj.ROUND_RHE if rng.integers(0, 2) else mj.ROUND_LEGACY
+        q, sc = mj.quantize_rowwise_int8(to_dev(W, dev), rounding)
+        rq, rs = (oracle_quantize_rowwise(W, rounding))
+        got = np.concatenate([q.cpu().numpy().view(np.uint8).ravel(), sc.cpu().numpy().view(np.uint8)])
+        ref = np.concatenate([rq.view(np.uint8).ravel(), rs.view(np.uint8)])
+        return (fam, N, K, rounding), got, ref
+    elif fam == "qtensor":
+        # per-tensor legacy quantize: near-ties (k + 1/2) s, random values,
+        # a tail of n % 4 elements, sometimes a view that is not 16-byte aligned
+        n, off = int(rng.integers(1, 3_000_001)), int(rng.integers(0, 2))
+        sv = np.float32(10.0 ** rng.uniform(-4, 1))
+        k = rng.integers(-300, 300, n + off) + 0.5
+        x = np.where(rng.random(n + off) < 0.5, k * sv,
+                     rng.standard_normal(n + off) * 100 * sv).astype(np.float32)
+        got = mj.quantize_symmetric_int8(mj.Tensor(to_dev(x, dev)[off:]), float(sv)).numpy()
+        return (fam, n, off, float(sv)), got, oracle_quantize_tensor(x[off:], sv)
     else:
         M, N, K = (int(v) for v in rng.integers(1, 3000, size=3))
         ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
@@ -278,9 +307,12 @@ def _long_case(rng, fam, dev, to_bf16):
 def test_long_random_sweep(oracle, dev):
     rng = np.random.default_rng(int(os.environ.get("MJ_LONG_SWEEP_SEED", "7")))
     t_end, n, bad = time.time() + _LONG, 0, []
-    fams = ("w8a16", "bf16", "i8", "f32")
+    fams = ("w8a16", "bf16", "i8", "f32", "qrow", "qtensor")
+    qrow = lambda W, r: oracle.quantize_rowwise_rhe(W) if r == mj.ROUND_RHE else \
+        oracle.quantize_rowwise_legacy(W)  # noqa: E731
     while time.time() < t_end:
-        desc, got, ref = _long_case(rng, fams[n % 4], dev, oracle.f32_to_bf16)
+        desc, got, ref = _long_case(rng, fams[n % len(fams)], dev, oracle.f32_to_bf16, qrow,
+                                    oracle.quantize_symmetric_int8)
         n += 1
         if got.shape != ref.shape or not np.array_equal(got, ref):
             bad.append(desc)
