@@ -30,12 +30,6 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// 16-byte streaming load (nontemporal: the data is read once).
-__device__ __forceinline__ uint4 load_nt16(const void *p) {
-  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-
 __device__ __forceinline__ float4 load_nt16f(const void *p) {
   const f32x4 v = __builtin_nontemporal_load((const f32x4 *)p);
   return make_float4(v[0], v[1], v[2], v[3]);

@@ -244,7 +244,10 @@ __device__ __forceinline__ uint32_t quant_pair2(uint32_t w0, uint32_t w1, float 
 // W waves per row (W = 1, 2 or 4; 4 / W rows per workgroup), CH 16-byte
 // loads per lane: K = 512 W CH.  Several waves per row keep more loads in
 // flight than one wave holding the whole row (the kernel is latency-bound at
-// C4's 2048 rows with one); the row's absmax is combined through LDS.
+// C4's 2048 rows with one); the row's absmax is combined through LDS.  x is
+// an activation the previous layer has just written, so it is read with
+// plain loads (nontemporal ones measured 3 % slower: 9.08 against 8.82 us
+// for C4's 2048 x 4096 on MI355X).
 template <int W, int CH>
 __global__ __launch_bounds__(256) void quantize_rows_bf16_reg(const uint16_t *__restrict__ x,
                                                               int M, int K,
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(256) void quantize_rows_bf16_reg(const uint16_t *__
   uint4 v[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c)
-    v[c] = live ? load_nt16(x4 + c * 64 * W + t) : make_uint4(0, 0, 0, 0);
+    v[c] = live ? x4[c * 64 * W + t] : make_uint4(0, 0, 0, 0);
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) amax = fmaxf(amax, amax8(v[c]));
