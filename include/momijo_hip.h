@@ -16,6 +16,17 @@
  * reference's Linear layout [out_features, in_features] (learn/nn/layers.mojo:
  * 347-348), so y = x W^T is an "NT" product.
  *
+ * Workspace.  Calls that need scratch device memory (the split-K W8A16 and
+ * bf16 GEMMs, the FFN when it splits K, QuantLinear, the W8A8 Linear,
+ * Linear.backward's column sums for N > 1024, the min/max observer) take it
+ * from one buffer per (device, stream) that the library keeps and grows;
+ * hipStreamPerThread gets one per (device, host thread).  A call holds that
+ * buffer from its first to its last enqueue, so host threads may share a
+ * stream.  While `stream` is being captured into a HIP graph these calls
+ * return MJ_ERR_UNSUPPORTED and enqueue nothing: the library never allocates
+ * on a capturing stream.  Everything else (the GEMV, GEMMs without a K split,
+ * quantizers, mj_quant_linear_f32_noalloc) can be captured.
+ *
  * Reference citations are relative to /root/reference/legacy/src/momijo/.
  */
 #ifndef MOMIJO_HIP_H
@@ -181,6 +192,18 @@ int32_t mj_launch_linear_bw_db_h(const float *dy, float *db, int64_t N, int64_t 
  * Replaces Tensor.relu / silu / gelu (tensor/tensor.mojo:3848,4003,4020 ->
  * apply_unary, tensor/math.mojo:566-638) and ReLU.forward (layers.mojo:134). */
 int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream);
+
+/* y = x >= s ? x : s over n fp32 elements (may alias): -0 stays -0 at s = 0,
+ * NaN gives s.  Replaces Tensor[Float32].maximum_scalar(s) =
+ * where_f32(ge_t(self, s), self, s) (tensor/tensor.mojo:4232), which
+ * Converted.forward applies between the quantized layers
+ * (learn/api/sequential.mojo:423). */
+int32_t mj_maximum_scalar_f32(const float *x, float s, float *y, int64_t n, void *stream);
+
+/* y = Float32(x) over n int64 elements, rounded to nearest even.  Replaces
+ * astype_f32_from_int (tensor/cast.mojo:5431-5437), the upcast of
+ * Tensor[Int].matmul / matmul_vec (tensor/tensor.mojo:3161-3165,3174-3178). */
+int32_t mj_cast_i64_f32(const int64_t *x, float *y, int64_t n, void *stream);
 
 /* ---- bf16 -------------------------------------------------------------- */
 

@@ -12,7 +12,9 @@
 #include "abi_util.h"
 
 #include <atomic>
+#include <memory>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 // Scratch of mj_quant_linear_f32_noalloc: the int8 copy of x lives in this
@@ -55,62 +57,40 @@ int32_t noalloc_scratch(int8_t **out) {
   return MJ_OK;
 }
 
-// Workspace of the split-K partials, of QuantLinear's int8 copy of x and of
-// the W8A8 Linear's int8 x and row scales: one device buffer per (device,
-// stream), kept by the library and reused by every later call on that stream,
-// so such a call makes no allocation call once its stream has seen a call of
-// that size (calls on one stream are ordered, so they never overlap in it).
+// Workspace of the split-K partials, of QuantLinear's int8 copy of x, of the
+// W8A8 Linear's int8 x and row scales, and of the column-sum and min/max
+// partials: one device buffer per (device, stream), kept by the library and
+// reused by every later call on that stream, so such a call makes no
+// allocation call once its stream has seen a call of that size.  The one
+// handle value hipStreamPerThread names a different stream on each host
+// thread, so its buffers are kept per (device, thread).
+// A call holds its buffer's lock from acquiring it until its last kernel is
+// enqueued: kernels on one stream run in enqueue order, so two host threads
+// sharing a stream cannot interleave their kernels between one call's writes
+// and reads of the buffer.
 // A buffer that has to grow is replaced by one of at least twice its size; the
 // old one is kept until the process ends, since work already queued on the
 // stream may still read it.  A stream handle that is destroyed and created
-// again inherits the buffer: a split-K GEMM still running on the destroyed
-// stream must have finished first.  These calls are refused under graph
-// capture (MJ_ERR_UNSUPPORTED): a graph replayed on another stream would
-// share the buffer with eager calls; capture-safe callers use the entry
+// again inherits the buffer: work still running on the destroyed stream must
+// have finished first.  These calls are refused under graph capture
+// (MJ_ERR_UNSUPPORTED) before anything is enqueued: the library allocates
+// nothing on a capturing stream, and a graph replayed on another stream would
+// share the buffer with eager calls.  Capture-safe callers use the entry
 // points that need no workspace, or mj_quant_linear_f32_noalloc.
 struct StreamWorkspace {
-  int dev;
-  hipStream_t stream;
-  void *ptr;
-  size_t bytes;
+  int dev = 0;
+  hipStream_t stream = nullptr;
+  std::thread::id thread;  // the calling thread for hipStreamPerThread
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  std::mutex mu;           // held by the call using the buffer
 };
-std::mutex g_ws_mu;
-std::vector<StreamWorkspace> g_ws;
+std::mutex g_ws_mu;        // guards g_ws and g_ws_retired
+std::vector<std::unique_ptr<StreamWorkspace>> g_ws;
 std::vector<void *> g_ws_retired;
 
-int32_t stream_workspace(size_t bytes, hipStream_t stream, void **out) {
-  int dev = 0;
-  if (int32_t st = hip_status(hipGetDevice(&dev), "hipGetDevice")) return st;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  StreamWorkspace *e = nullptr;
-  for (auto &w : g_ws)
-    if (w.dev == dev && w.stream == stream) e = &w;
-  if (e && e->bytes >= bytes) {
-    *out = e->ptr;
-    return MJ_OK;
-  }
-  size_t want = bytes;
-  if (e && want < 2 * e->bytes) want = 2 * e->bytes;
-  want = (want + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
-  void *p = nullptr;
-  if (hipMalloc(&p, want) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "split-K workspace allocation of %zu bytes failed", want);
-  }
-  if (e) {
-    g_ws_retired.push_back(e->ptr);
-    e->ptr = p;
-    e->bytes = want;
-  } else {
-    g_ws.push_back({dev, stream, p, want});
-  }
-  *out = p;
-  return MJ_OK;
-}
-
-// Workspace of `bytes` for work enqueued on `stream` (stream_workspace);
-// MJ_ERR_UNSUPPORTED while the stream is being captured into a graph.
-int32_t acquire_workspace(size_t bytes, hipStream_t stream, void **out) {
+// MJ_ERR_UNSUPPORTED (and nothing enqueued) while `stream` is being captured.
+int32_t refuse_capture(hipStream_t stream) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (int32_t st = hip_status(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing"))
     return st;
@@ -119,24 +99,90 @@ int32_t acquire_workspace(size_t bytes, hipStream_t stream, void **out) {
                 "this call needs the library's per-stream workspace, which is not available "
                 "under graph capture (mj_quant_linear_f32_noalloc, the GEMV (M <= 16) and "
                 "the GEMMs without a K split can be captured)");
-  return stream_workspace(bytes, stream, out);
+  return MJ_OK;
 }
 
-// Plans and launches an NT GEMM, with the fp32 workspace of the stream when
-// the plan splits K.
-int32_t run_gemm_nt(mj::GemmNT p, hipStream_t stream, const char *what) {
-  // The tile kernels address a tile's 256 rows of A and of B with 32-bit
-  // buffer offsets ((r * ld + k) * element size, r < 256): larger leading
-  // dimensions would wrap or fall outside the buffer resource and read zeros.
+// The workspace of one call: acquire() refuses capture, finds or grows the
+// buffer of (device, stream) and locks it until the lease is destroyed, i.e.
+// until the call has enqueued its kernels.
+class WorkspaceLease {
+ public:
+  void *ptr = nullptr;
+
+  int32_t acquire(size_t bytes, hipStream_t stream) {
+    if (int32_t st = refuse_capture(stream)) return st;
+    int dev = 0;
+    if (int32_t st = hip_status(hipGetDevice(&dev), "hipGetDevice")) return st;
+    const std::thread::id me =
+        stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    StreamWorkspace *e = nullptr;
+    {
+      std::lock_guard<std::mutex> g(g_ws_mu);
+      for (auto &w : g_ws)
+        if (w->dev == dev && w->stream == stream && w->thread == me) e = w.get();
+      if (!e) {
+        g_ws.push_back(std::make_unique<StreamWorkspace>());
+        e = g_ws.back().get();
+        e->dev = dev;
+        e->stream = stream;
+        e->thread = me;
+      }
+    }
+    lock_ = std::unique_lock<std::mutex>(e->mu);
+    if (e->bytes < bytes) {
+      size_t want = bytes;
+      if (want < 2 * e->bytes) want = 2 * e->bytes;
+      want = (want + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
+      void *p = nullptr;
+      if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        lock_.unlock();
+        return fail(MJ_ERR_ALLOC, "workspace allocation of %zu bytes failed", want);
+      }
+      if (e->ptr) {
+        std::lock_guard<std::mutex> g(g_ws_mu);
+        g_ws_retired.push_back(e->ptr);
+      }
+      e->ptr = p;
+      e->bytes = want;
+    }
+    ptr = e->ptr;
+    return MJ_OK;
+  }
+
+ private:
+  std::unique_lock<std::mutex> lock_;
+};
+
+// Launches a planned NT GEMM; `part` is the fp32 workspace when the plan
+// splits K.
+int32_t launch_planned(mj::GemmNT p, const mj::GemmPlan &plan, void *part, hipStream_t stream,
+                       const char *what) {
+  p.part = (float *)part;
+  return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+}
+
+// The tile kernels address a tile's 256 rows of A and of B with 32-bit
+// buffer offsets ((r * ld + k) * element size, r < 256): larger leading
+// dimensions would wrap or fall outside the buffer resource and read zeros.
+int32_t check_tile_offsets(const mj::GemmNT &p, const char *what) {
   const int64_t bsz = p.bkind == mj::B_INT8 ? 1 : 2;
   if (256 * p.lda * 2 >= ((int64_t)1 << 31) || 256 * p.ldb * bsz >= ((int64_t)1 << 31))
     return fail(MJ_ERR_UNSUPPORTED, "%s: leading dimension too large for 32-bit tile offsets "
                 "(lda=%lld, ldb=%lld)", what, (long long)p.lda, (long long)p.ldb);
+  return MJ_OK;
+}
+
+// Plans and launches an NT GEMM, with the fp32 workspace of the stream when
+// the plan splits K.
+int32_t run_gemm_nt(const mj::GemmNT &p, hipStream_t stream, const char *what) {
+  if (int32_t st = check_tile_offsets(p, what)) return st;
   const mj::GemmPlan plan = mj::plan_gemm_nt(p);
   const size_t ws = plan.workspace_bytes(p);
-  if (!ws) return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
-  if (int32_t st = acquire_workspace(ws, stream, (void **)&p.part)) return st;
-  return hip_status(mj::launch_gemm_nt(p, plan, stream), what);
+  if (!ws) return launch_planned(p, plan, nullptr, stream, what);
+  WorkspaceLease lease;
+  if (int32_t st = lease.acquire(ws, stream)) return st;
+  return launch_planned(p, plan, lease.ptr, stream, what);
 }
 
 // QuantLinear.forward on a caller-provided int8 buffer xq of M*K bytes
@@ -162,21 +208,12 @@ int32_t quant_linear_body(const float *x, const int8_t *Wq, const float *b, floa
                     "gemm_i8 scalar launch");
 }
 
-// db = column sums of dy [N, OutF], with a stream-ordered workspace when the
-// rows are split into segments.
-int32_t run_colsum(const float *dy, int64_t N, int64_t OutF, float *db, hipStream_t stream) {
+// db = column sums of dy [N, OutF]; `part` holds the segment partials when
+// colsum_segments(N, OutF) > 1 (the caller's workspace lease).
+int32_t run_colsum(const float *dy, int64_t N, int64_t OutF, float *db, float *part,
+                   hipStream_t stream) {
   const int64_t segs = mj::colsum_segments(N, OutF);
-  float *part = nullptr;
-  if (segs > 1 &&
-      hipMallocAsync((void **)&part, (size_t)segs * (size_t)OutF * sizeof(float), stream) !=
-          hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "column-sum workspace allocation failed");
-  }
-  const int32_t st =
-      hip_status(mj::launch_colsum_f32(dy, N, OutF, db, part, segs, stream), "colsum launch");
-  if (part) (void)hipFreeAsync(part, stream);
-  return st;
+  return hip_status(mj::launch_colsum_f32(dy, N, OutF, db, part, segs, stream), "colsum launch");
 }
 
 }  // namespace
@@ -328,6 +365,13 @@ int32_t mj_linear_backward_f32(const float *x, const float *W, const float *dy, 
   if (want_dx && OutF > 0 && !W) return fail(MJ_ERR_ARG, "null W");
   if (want_dW && N > 0 && !x) return fail(MJ_ERR_ARG, "null x");
   const hipStream_t st = S(stream);
+  // the column-sum partials: acquired before anything is enqueued, so a
+  // refusal (graph capture) leaves the stream untouched
+  WorkspaceLease lease;
+  const int64_t segs = want_db ? mj::colsum_segments(N, OutF) : 1;
+  if (segs > 1) {
+    if (int32_t e = lease.acquire((size_t)segs * (size_t)OutF * sizeof(float), st)) return e;
+  }
   // dx [N, InF] = dy [N, OutF] @ W [OutF, InF]
   if (want_dx) {
     if (int32_t e = hip_status(mj::launch_gemm_f32(N, InF, OutF, dy, OutF, 1, W, InF, 1, nullptr,
@@ -342,7 +386,7 @@ int32_t mj_linear_backward_f32(const float *x, const float *W, const float *dy, 
                                "linear backward dW"))
       return e;
   }
-  if (want_db) return run_colsum(dy, N, OutF, db, st);
+  if (want_db) return run_colsum(dy, N, OutF, db, (float *)lease.ptr, st);
   return MJ_OK;
 }
 
@@ -440,6 +484,21 @@ int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n,
   return hip_status(mj::launch_activation_f32(epilogue, x, y, n, S(stream)), "activation launch");
 }
 
+int32_t mj_maximum_scalar_f32(const float *x, float s, float *y, int64_t n, void *stream) {
+  if (n < 0) return fail(MJ_ERR_ARG, "negative size");
+  if (n == 0) return MJ_OK;
+  if (!x || !y) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_maximum_scalar_f32(x, s, y, n, S(stream)),
+                    "maximum_scalar launch");
+}
+
+int32_t mj_cast_i64_f32(const int64_t *x, float *y, int64_t n, void *stream) {
+  if (n < 0) return fail(MJ_ERR_ARG, "negative size");
+  if (n == 0) return MJ_OK;
+  if (!x || !y) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_cast_i64_f32(x, y, n, S(stream)), "cast launch");
+}
+
 // ------------------------------------------------------------------ bf16
 int32_t mj_gemm_bf16_nt(int64_t M, int64_t N, int64_t K, const uint16_t *A, int64_t lda,
                         const uint16_t *B, int64_t ldb, const float *bias, int32_t epilogue,
@@ -470,31 +529,23 @@ int32_t mj_quantize_symmetric_int8(const float *x, int64_t n, float scale, int8_
 int32_t mj_minmax_f32(const float *x, int64_t n, float *minmax_out, void *stream) {
   if (n <= 0) return fail(MJ_ERR_ARG, "minmax needs n > 0");
   if (!x || !minmax_out) return fail(MJ_ERR_ARG, "null operand");
-  float *part = nullptr;
-  const size_t bytes = sizeof(float) * 2 * mj::minmax_partials();
-  if (hipMallocAsync((void **)&part, bytes, S(stream)) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
-  }
-  int32_t st = hip_status(mj::launch_minmax(x, n, part, minmax_out, S(stream)), "minmax launch");
-  (void)hipFreeAsync(part, S(stream));
-  return st;
+  WorkspaceLease lease;
+  if (int32_t st = lease.acquire(sizeof(float) * 2 * mj::minmax_partials(), S(stream)))
+    return st;
+  return hip_status(mj::launch_minmax(x, n, (float *)lease.ptr, minmax_out, S(stream)),
+                    "minmax launch");
 }
 
 int32_t mj_minmax_scale_symmetric(const float *x, int64_t n, float max_q, float *scale_out,
                                   void *stream) {
   if (n < 0) return fail(MJ_ERR_ARG, "negative size");
   if (!scale_out || (n > 0 && !x)) return fail(MJ_ERR_ARG, "null operand");
-  float *part = nullptr;
-  const size_t bytes = sizeof(float) * 2 * mj::minmax_partials();
-  if (hipMallocAsync((void **)&part, bytes, S(stream)) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(MJ_ERR_ALLOC, "workspace allocation failed");
-  }
-  int32_t st = hip_status(mj::launch_minmax_scale(x, n, max_q, part, scale_out, S(stream)),
-                          "minmax launch");
-  (void)hipFreeAsync(part, S(stream));
-  return st;
+  WorkspaceLease lease;
+  if (int32_t st = lease.acquire(sizeof(float) * 2 * mj::minmax_partials(), S(stream)))
+    return st;
+  return hip_status(
+      mj::launch_minmax_scale(x, n, max_q, (float *)lease.ptr, scale_out, S(stream)),
+      "minmax launch");
 }
 
 int32_t mj_matmul_i8_i8_to_i32(const int8_t *A, const int8_t *B, int32_t *C, int64_t M,
@@ -536,9 +587,10 @@ int32_t mj_quant_linear_f32(const float *x, const int8_t *Wq, const float *b, fl
   if (M == 0 || N == 0) return MJ_OK;
   if (!y || !b || (K > 0 && (!x || !Wq))) return fail(MJ_ERR_ARG, "null operand");
   // the int8 copy of x in the stream's workspace
-  int8_t *xq = nullptr;
-  if (int32_t st = acquire_workspace((size_t)M * K + 16, S(stream), (void **)&xq)) return st;
-  return quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, xq, S(stream));
+  WorkspaceLease lease;
+  if (int32_t st = lease.acquire((size_t)M * K + 16, S(stream))) return st;
+  return quant_linear_body(x, Wq, b, s_w, s_x, y, M, N, K, legacy_literal, (int8_t *)lease.ptr,
+                           S(stream));
 }
 
 int32_t mj_quant_linear_f32_noalloc(const float *x, const int8_t *Wq, const float *b, float s_w,
@@ -613,10 +665,9 @@ int32_t mj_linear_w8a8(const uint16_t *x, const int8_t *Q, const float *scales, 
                 "W8A8 Linear needs K %% 16 == 0, K <= 131072 and 16-byte aligned x, Q");
   // xq [M,K] int8 then sx [M] fp32 in the stream's workspace
   const size_t xq_bytes = ((size_t)M * K + 255) & ~(size_t)255;
-  int8_t *ws = nullptr;
-  if (int32_t st = acquire_workspace(xq_bytes + (size_t)M * sizeof(float), S(stream),
-                                     (void **)&ws))
-    return st;
+  WorkspaceLease lease;
+  if (int32_t st = lease.acquire(xq_bytes + (size_t)M * sizeof(float), S(stream))) return st;
+  int8_t *ws = (int8_t *)lease.ptr;
   float *sx = (float *)(ws + xq_bytes);
   int32_t st = hip_status(mj::launch_quantize_rows_bf16(x, M, K, ws, sx, S(stream)),
                           "quantize_rows_bf16 launch");
@@ -641,15 +692,35 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   mj::GemmNT gu;
   gu.A = x; gu.lda = K; gu.B = Wg; gu.B2 = Wu; gu.ldb = K; gu.scales = sg; gu.scales2 = su;
   gu.C = h; gu.ldc = I; gu.M = M; gu.N = I; gu.K = K; gu.bkind = mj::B_INT8; gu.gate_up = true;
-  if (int32_t st = run_gemm_nt(gu, S(stream), "gate/up")) return st;
-  if (M <= mj::kGemvMaxM)
-    return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
-                                            S(stream)),
-                      "down gemv launch");
   mj::GemmNT dn;
   dn.A = h; dn.lda = I; dn.B = Wd; dn.ldb = I; dn.scales = sd; dn.C = y; dn.ldc = H;
   dn.M = M; dn.N = H; dn.K = I; dn.bkind = mj::B_INT8;
-  return run_gemm_nt(dn, S(stream), "down");
+  const bool down_gemv = M <= mj::kGemvMaxM;
+  if (int32_t st = check_tile_offsets(gu, "gate/up")) return st;
+  if (!down_gemv) {
+    if (int32_t st = check_tile_offsets(dn, "down")) return st;
+  }
+  // both plans first: one workspace of the larger size is acquired before
+  // anything is enqueued (the two GEMMs run in order on the stream, so they
+  // can share it)
+  const mj::GemmPlan pgu = mj::plan_gemm_nt(gu);
+  mj::GemmPlan pdn;
+  size_t ws = pgu.workspace_bytes(gu);
+  if (!down_gemv) {
+    pdn = mj::plan_gemm_nt(dn);
+    const size_t wd = pdn.workspace_bytes(dn);
+    if (wd > ws) ws = wd;
+  }
+  WorkspaceLease lease;
+  if (ws) {
+    if (int32_t st = lease.acquire(ws, S(stream))) return st;
+  }
+  if (int32_t st = launch_planned(gu, pgu, lease.ptr, S(stream), "gate/up")) return st;
+  if (down_gemv)
+    return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
+                                            S(stream)),
+                      "down gemv launch");
+  return launch_planned(dn, pdn, lease.ptr, S(stream), "down");
 }
 
 }  // extern "C"

@@ -478,4 +478,43 @@ hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,
   return hipGetLastError();
 }
 
+// Tensor[Float32].maximum_scalar(s) = where(x >= s, x, s)
+// (tensor/tensor.mojo:4232): x itself where x >= s (so -0 stays -0 at s = 0),
+// else s (NaN >= s is false, so NaN gives s).
+__global__ __launch_bounds__(256) void maximum_scalar_f32_kernel(const float *x, float s, float *y,
+                                                                 int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = x[i];
+    y[i] = v >= s ? v : s;
+  }
+}
+
+hipError_t launch_maximum_scalar_f32(const float *x, float s, float *y, int64_t n,
+                                     hipStream_t stream) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(maximum_scalar_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x,
+                     s, y, n);
+  return hipGetLastError();
+}
+
+// astype_f32_from_int (tensor/cast.mojo:5431-5437): Float32(Int) of each
+// 64-bit element, rounded to nearest even (the conversion rounds once, from
+// the exact integer).
+__global__ __launch_bounds__(256) void cast_i64_f32_kernel(const int64_t *x, float *y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (float)x[i];
+}
+
+hipError_t launch_cast_i64_f32(const int64_t *x, float *y, int64_t n, hipStream_t stream) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(cast_i64_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, y, n);
+  return hipGetLastError();
+}
+
 }  // namespace mj

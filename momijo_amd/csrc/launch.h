@@ -89,6 +89,11 @@ hipError_t launch_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, 
                              const float *x, int64_t sx, float *y, hipStream_t stream);
 hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,
                                  hipStream_t stream);
+// y = x >= s ? x : s elementwise (Tensor[Float32].maximum_scalar).
+hipError_t launch_maximum_scalar_f32(const float *x, float s, float *y, int64_t n,
+                                     hipStream_t stream);
+// y = Float32(x) elementwise, round to nearest even (astype_f32_from_int).
+hipError_t launch_cast_i64_f32(const int64_t *x, float *y, int64_t n, hipStream_t stream);
 
 // ---- gemv_w8.hip: skinny-M W8A16 -----------------------------------------
 // Largest x row count the W8A16 GEMV kernels take; larger M runs the int8

@@ -88,10 +88,12 @@ class Linear:
 
 
 class ReLU:
-    """ReLU.forward = _maximum_scalar(x, 0): v > 0 ? v : 0 (layers.mojo:117-137)."""
+    """ReLU.forward = layers.mojo's own _maximum_scalar(x, 0): v > 0 ? v : 0
+    (layers.mojo:117-137), so -0 and NaN give +0 -- unlike
+    Tensor.maximum_scalar(0), which keeps -0."""
 
     def forward(self, x: Tensor) -> Tensor:
-        return x.maximum_scalar(0.0)
+        return x._unary(_lib.EPI_RELU)
 
 
 class QuantLinear:
@@ -208,7 +210,17 @@ class W8MLP:
     silu(g) * u; the down projection is a second W8A16 GEMM."""
 
     def __init__(self, gate: W8Linear, up: W8Linear, down: W8Linear):
-        assert gate.q.shape == up.q.shape and down.in_features == gate.out_features
+        # the C ABI reads Wu with Wg's shape and Wd as [H, I]: a mismatch
+        # would read past the weights, so it is refused here
+        if tuple(gate.q.shape) != tuple(up.q.shape):
+            raise ValueError(f"gate and up weights differ in shape: {list(gate.q.shape)} vs "
+                             f"{list(up.q.shape)}")
+        if down.in_features != gate.out_features:
+            raise ValueError(f"down takes {down.in_features} features, gate/up give "
+                             f"{gate.out_features}")
+        for name, lin in (("gate", gate), ("up", up), ("down", down)):
+            if lin.scales.dtype != torch.float32 or lin.scales.numel() != lin.out_features:
+                raise ValueError(f"{name} scales must be float32 with {lin.out_features} elements")
         self.gate, self.up, self.down = gate, up, down
 
     def forward(self, x: torch.Tensor, h: torch.Tensor | None = None,

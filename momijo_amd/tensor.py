@@ -149,13 +149,17 @@ class Tensor:
         return self._unary(_lib.EPI_SILU)
 
     def maximum_scalar(self, s: float) -> "Tensor":
-        """maximum_scalar(0.0) as used between quantized layers
-        (learn/api/sequential.mojo:423).  Only s == 0 is on this path; it is
-        evaluated as v > 0 ? v : 0, equal in value to the reference's
-        where(v >= 0, v, 0) (the two differ only in the sign of a zero)."""
-        if s != 0.0:
-            raise NotImplementedError("maximum_scalar is provided for s == 0 only")
-        return self._unary(_lib.EPI_RELU)
+        """Tensor[Float32].maximum_scalar(s) = where_f32(ge_t(self, s), self, s)
+        (tensor/tensor.mojo:4232): x where x >= s, else s, so -0 stays -0 at
+        s = 0 and NaN becomes s.  Converted.forward applies it with s = 0
+        between the quantized layers (learn/api/sequential.mojo:423)."""
+        if self._t.dtype != torch.float32:
+            raise TypeError("maximum_scalar is provided for Float32 tensors")
+        src = self._t.contiguous()
+        out = torch.empty_like(src)
+        _lib.call("mj_maximum_scalar_f32", _ptr(src), float(np.float32(s)), _ptr(out),
+                  src.numel(), _stream())
+        return Tensor(out)
 
     def __repr__(self) -> str:
         return f"Tensor(shape={self.shape()}, dtype={self._t.dtype})"
@@ -174,13 +178,23 @@ def empty_f64() -> Tensor:
 _INT_DTYPES = (torch.int64, torch.int32)
 
 
+def astype_f32_from_int(t: torch.Tensor) -> torch.Tensor:
+    """astype_f32_from_int (tensor/cast.mojo:5431-5437): Float32(Int) of every
+    element, rounded to nearest even, by the library's cast kernel.  The
+    reference walks its flat storage in order; a view is taken in logical
+    (row-major) order here, as its shape says."""
+    src = t.to(torch.int64).contiguous()
+    out = torch.empty(src.shape, dtype=torch.float32, device=src.device)
+    _lib.call("mj_cast_i64_f32", _ptr(src), _ptr(out), src.numel(), _stream())
+    return out
+
+
 def _upcast_int_pair(A: Tensor, B: Tensor) -> tuple[Tensor, Tensor]:
     """Tensor[Int] @ Tensor[Int] -> Float32: both operands are converted with
-    astype_f32_from_int (tensor/tensor.mojo:3161-3165, 3174-3178: a
-    round-to-nearest Float32(Int) cast, here torch's int-to-float cast on the
-    device), then the Float32 product runs.  Other dtypes pass through."""
+    astype_f32_from_int (tensor/tensor.mojo:3161-3165, 3174-3178), then the
+    Float32 product runs.  Other dtypes pass through."""
     if A._t.dtype in _INT_DTYPES and B._t.dtype in _INT_DTYPES:
-        return Tensor(A._t.to(torch.float32)), Tensor(B._t.to(torch.float32))
+        return Tensor(astype_f32_from_int(A._t)), Tensor(astype_f32_from_int(B._t))
     return A, B
 
 

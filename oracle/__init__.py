@@ -19,6 +19,11 @@ Parity status of each restated function (how it is pinned, see
   contraction choice is **parity unpinned** at the last ulp.
 * relu / gelu32 / silu32 / sigmoid32 / tanh32: closed forms against libm in
   double.  The Mojo stdlib ``exp`` ulp behaviour is **parity unpinned**.
+* maximum_scalar_f32: the -0 / NaN / equal-to-s cases against the mask rule
+  x >= s written out, plus numpy's fmax away from those cases.
+* astype_f32_from_int: integers above 2^24 with exact ties (2^24 + 1 -> 2^24,
+  2^24 + 3 -> 2^24 + 4), 2^63 - 1, negatives, and numpy's int64 -> float32
+  cast (round to nearest even) on random 64-bit integers.
 * _exp_approx family: exact IEEE op sequence, pinned against a numpy float32
   restatement.
 * quantize_symmetric_int8 / matmul_i8_i8_to_i32 / dequantize / minmax scale:
@@ -89,6 +94,8 @@ def _declare(L):
         "mo_linear_act_f32": (None, [_P, _P, _P, _I, _I, _P, _I64, _I64, _I64]),
         "mo_epilogue32_n": (None, [_I, _P, _P, _I64]),
         "mo_gelu32_n": (None, [_P, _P, _I64]),
+        "mo_maximum_scalar32_n": (None, [_P, _F, _P, _I64]),
+        "mo_astype_f32_from_int": (None, [_P, _P, _I64]),
         "mo_exp_approx32": (_F, [_F]),
         "mo_tanh_approx32": (_F, [_F]),
         "mo_quant_legacy_one": (ctypes.c_int8, [_F, _F]),
@@ -161,6 +168,23 @@ def randn_f32_f32core(shape, seed=0) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().mo_randn_f32_f32core(_ptr(out), n, seed)
     return out.reshape(shape)
+
+
+# ----------------------------------------------------------------- elementwise
+def maximum_scalar_f32(x, s: float) -> np.ndarray:
+    """Tensor[Float32].maximum_scalar(s) (tensor/tensor.mojo:4232)."""
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.float32)
+    lib().mo_maximum_scalar32_n(_ptr(x), float(np.float32(s)), _ptr(y), x.size)
+    return y
+
+
+def astype_f32_from_int(x) -> np.ndarray:
+    """astype_f32_from_int (tensor/cast.mojo:5431-5437) of an int64 array."""
+    x = _c(x, np.int64)
+    y = np.empty(x.shape, np.float32)
+    lib().mo_astype_f32_from_int(_ptr(x), _ptr(y), x.size)
+    return y
 
 
 # ----------------------------------------------------------------- bf16

@@ -282,6 +282,20 @@ MO_API float mo_relu_layer32(float v) { return v > 0.0f ? v : 0.0f; }
  * if v < 0: v = 0  (NaN stays NaN, -0 stays -0). */
 MO_API float mo_relu_unary32(float v) { return v < 0.0f ? 0.0f : v; }
 
+/* Tensor[Float32].maximum_scalar(s) = where_f32(ge_t(self, s), self, s)
+ * (tensor/tensor.mojo:4232): the mask x >= s picks x, else s (NaN >= s is
+ * false; -0 >= 0 is true, so -0 stays). */
+MO_API void mo_maximum_scalar32_n(const float *x, float s, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] >= s ? x[i] : s;
+}
+
+/* astype_f32_from_int (tensor/cast.mojo:5431-5437): flat.append(Float32(v))
+ * for each Int of the storage in order; the C conversion of a 64-bit integer
+ * rounds to nearest even under the default rounding mode. */
+MO_API void mo_astype_f32_from_int(const int64_t *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = (float)x[i];
+}
+
 /* sigmoid32 / tanh32 / silu32 / gelu32 (tensor/math.mojo:272-295) with
  * exp32 = stdlib exp on Float32 (math.mojo:490).  tanh32 is the literal
  * (e^{2t}-1)/(e^{2t}+1), which is NaN once e^{2t} overflows (t > ~44.36,

@@ -128,3 +128,40 @@ def test_int_tensor_matmul_upcasts_to_float32(oracle, dev):
     assert v.dtype == torch.float32
     np.testing.assert_array_equal(v.numpy(), oracle.matvec_f32(A.astype(np.float32),
                                                                x.astype(np.float32)))
+
+
+def test_int_upcast_rounds_like_astype_f32_from_int(oracle, dev):
+    """Integers beyond 2^24 round to nearest even in the library's cast
+    kernel, as astype_f32_from_int does (tensor/cast.mojo:5431-5437); the
+    product then runs on the rounded Float32 values."""
+    p24 = 1 << 24
+    vals = np.array([p24 + 1, p24 + 3, -(p24 + 1), (1 << 40) + (1 << 16),
+                     (1 << 40) + (1 << 16) + 1, (1 << 62) + 12345, -(1 << 63), 5], np.int64)
+    rng = np.random.default_rng(44)
+    big = rng.integers(-(1 << 63), (1 << 63) - 1, size=4096, dtype=np.int64)
+    got = mj.tensor.astype_f32_from_int(torch.from_numpy(np.concatenate([vals, big])).to(dev))
+    want = oracle.astype_f32_from_int(np.concatenate([vals, big]))
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    A = rng.integers(p24, 4 * p24, size=(6, 5))
+    B = rng.integers(-3, 4, size=(5, 3))
+    c = mj.Tensor(torch.from_numpy(A).to(dev)).matmul(mj.Tensor(torch.from_numpy(B).to(dev)))
+    # the rounded operands' products are not exact in fp32: the fp32 bar
+    assert_close_f32(c.numpy(), oracle.matmul_f32(oracle.astype_f32_from_int(A),
+                                                  oracle.astype_f32_from_int(B)))
+
+
+def test_maximum_scalar_keeps_negative_zero(oracle, dev):
+    """Tensor.maximum_scalar(s) = where(x >= s, x, s) (tensor/tensor.mojo:4232)
+    for s = 0 and other s, bit for bit (signed zeros, NaN, s itself)."""
+    x = np.concatenate([np.array([-0.0, 0.0, np.nan, -np.nan, np.inf, -np.inf, 0.25, -2.0],
+                                 np.float32),
+                        oracle.randn_f32((10_000,), seed=45)])
+    for s in (0.0, 0.25, -2.0, 1.5):
+        got = mj.Tensor(to_dev(x, dev)).maximum_scalar(s).numpy()
+        want = oracle.maximum_scalar_f32(x, s)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    y0 = mj.Tensor(to_dev(x, dev)).maximum_scalar(0.0).numpy()
+    assert np.signbit(y0[0]) and y0[2] == 0
+    # ReLU.forward (layers.mojo's _maximum_scalar: v > 0 ? v : 0) maps -0 to +0
+    r = mj.ReLU().forward(mj.Tensor(to_dev(x, dev))).numpy()
+    assert not np.signbit(r[0])
