@@ -21,8 +21,11 @@ weights from HBM.
 ``cpu_baseline`` times the oracle (the C restatement of momijo's CPU tensor
 engine, single-threaded as the reference is) on a row slab of C2, on this
 box's host cores, using the very bytes the GPU leg multiplied (copied back
-from the device after its timed region; sha256 recorded).  The C3 and C1
-entries carry their own ``cpu_baseline``, timed in full the same way.
+from the device after its timed region; sha256 recorded).  The C3, C3-pack
+and C1 entries carry their own ``cpu_baseline``, timed in full the same way;
+C4 and C5 carry one timed on a row slab of their x with the full weights
+(every row costs the same, so the slab's rate is the problem's; the full
+problem's time is extrapolated linearly in M and stated).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -116,6 +119,10 @@ def _rand_f32(shape, seed, std=1.0):
 # Inputs of the GPU legs that the CPU baseline re-times on the same bytes
 # (copied from the device after the timed region): name -> host arrays.
 _CPU_INPUTS = {}
+# Rows of x in the CPU legs' row slabs of C4 and C5 (each row costs the CPU
+# the same work, so the slab's rate is the full problem's rate).
+CPU_SLAB_C4 = 32
+CPU_SLAB_C5 = 8
 
 
 def _host_bf16_bits(t):
@@ -238,6 +245,7 @@ def bench_c3_pack(steps, warmup):
     ms = _time_launches(run, max(steps // 2, 20), warmup)
     bytes_ = N * K * 4 + N * K + N * 4
     gbs = bytes_ / (ms * 1e-3) / 1e9
+    _CPU_INPUTS["c3pack"] = (Ws[0].cpu().numpy(),)
     return {
         "name": "c3pack_quantize_rowwise_11008x4096",
         "metric": "per-channel int8 quantize/pack GB/s",
@@ -260,6 +268,8 @@ def bench_c4(steps, warmup):
     ms = _time_launches(lambda i: lin.forward(x, out=y), steps, warmup)
     flops = 2.0 * M * N * K
     tf = flops / (ms * 1e-3) / 1e12
+    _CPU_INPUTS["c4"] = (_host_bf16_bits(x[:CPU_SLAB_C4]), lin.q.cpu().numpy(),
+                         lin.scales.cpu().numpy(), lin.bias.cpu().numpy(), M)
     return {
         "name": "c4_w8a16_prefill_gelu_2048x4096x4096",
         "metric": "W8A16 GEMM + bias + GELU TFLOP/s",
@@ -309,6 +319,9 @@ def bench_c5(steps, warmup):
     ms = _time_launches(lambda i: mlp.forward(x, h, y), steps, warmup)
     flops = 3 * 2.0 * M * K * I
     tf = flops / (ms * 1e-3) / 1e12
+    _CPU_INPUTS["c5"] = (_host_bf16_bits(x[:CPU_SLAB_C5]), g.q.cpu().numpy(), g.scales.cpu().numpy(),
+                         u.q.cpu().numpy(), u.scales.cpu().numpy(), d.q.cpu().numpy(),
+                         d.scales.cpu().numpy(), M)
     return {
         "name": "c5_w8a16_mlp_512x4096x11008",
         "metric": "W8A16 Llama FFN TFLOP/s (gate/up + down)",
@@ -526,6 +539,66 @@ def cpu_baseline_c1():
             "input_sha256": _sha256(x, W, b)}
 
 
+def cpu_baseline_c3pack():
+    """The per-channel RHE quantize/pack restated in the oracle (a division
+    and rint per element, as the spec reads), timed in full on the GPU leg's
+    W, single thread."""
+    import oracle
+    oracle.build()
+    (W,) = _CPU_INPUTS["c3pack"]
+    per_call, n = _time_cpu(lambda: oracle.quantize_rowwise_rhe(W), 2.0)
+    N, K = W.shape
+    bytes_ = N * K * 4 + N * K + N * 4
+    return {"value": bytes_ / per_call / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_call": per_call * 1e3,
+            "sample": f"full C3-pack ({N} x {K} fp32 -> int8 + scales), {n} calls on the GPU "
+                      "leg's W (oracle mo_quantize_rowwise_rhe, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(W)}
+
+
+def cpu_baseline_c4():
+    """momijo's Linear loop (strict-k fp32 dot per output, bias after the sum,
+    layers.mojo:383-433) on the widened int8 weights with the GELU epilogue
+    (oracle mo_linear_w8a16), on a row slab of the GPU leg's x with its full
+    weights; every row costs the same, so the slab's rate is the problem's."""
+    import oracle
+    oracle.build()
+    x, Q, s, b, M = _CPU_INPUTS["c4"]
+    per_call, n = _time_cpu(lambda: oracle.linear_w8a16(x, Q, s, b, oracle.EPI_GELU_TANH), 2.0)
+    rows, K = x.shape
+    N = Q.shape[0]
+    flops = 2.0 * rows * N * K
+    return {"value": flops / per_call / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "ms_per_call": per_call * 1e3,
+            "full_problem_s": per_call * M / rows,
+            "sample": f"C4 row slab: rows 0..{rows - 1} of the GPU leg's x ({M} x {K}) times its "
+                      f"full int8 W ({N} x {K}) + bias + GELU, {n} calls; the full {M} rows "
+                      f"extrapolate linearly to {per_call * M / rows:.0f} s (oracle "
+                      "mo_linear_w8a16, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(x, Q, s, b)}
+
+
+def cpu_baseline_c5():
+    """The FFN restated in the oracle (gate/up dots, silu(g)*u rounded to
+    bf16, down dot; strict-k fp32 sums), on a row slab of the GPU leg's x
+    with its full weights."""
+    import oracle
+    oracle.build()
+    x, Wg, sg, Wu, su, Wd, sd, M = _CPU_INPUTS["c5"]
+    rows, K = x.shape
+    per_call, n = _time_cpu(lambda: oracle.mlp_w8a16(x, Wg, sg, Wu, su, Wd, sd), 2.0)
+    I = Wg.shape[0]
+    flops = 3 * 2.0 * rows * K * I
+    return {"value": flops / per_call / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "ms_per_call": per_call * 1e3,
+            "full_problem_s": per_call * M / rows,
+            "sample": f"C5 row slab: rows 0..{rows - 1} of the GPU leg's x ({M} x {K}) through "
+                      f"the full gate/up ({I} x {K}) and down ({Wd.shape[0]} x {I}) int8 "
+                      f"weights, {n} calls; the full {M} rows extrapolate linearly to "
+                      f"{per_call * M / rows:.0f} s (oracle mo_mlp_w8a16, gcc -O2, 1 thread)",
+            "input_sha256": _sha256(x, Wg, sg, Wu, su, Wd, sd)}
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -566,7 +639,9 @@ def main():
         if "c2" in _CPU_INPUTS:
             cpu = cpu_baseline_c2()
             print(f"# cpu baseline done: {cpu['value']:.2e} TFLOP/s", file=sys.stderr, flush=True)
-        for key, fn in (("c3", cpu_baseline_c3), ("c1", cpu_baseline_c1)):
+        for key, fn in (("c3", cpu_baseline_c3), ("c3pack", cpu_baseline_c3pack),
+                        ("c4", cpu_baseline_c4), ("c5", cpu_baseline_c5),
+                        ("c1", cpu_baseline_c1)):
             if key in _CPU_INPUTS:
                 entry = next(r for r in secondary if r["name"].startswith(key + "_"))
                 entry["cpu_baseline"] = fn()

@@ -33,6 +33,11 @@ CFLAGS = [
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # kernel arguments preloaded into SGPRs at wave launch (kernels with
+    # scalar arguments: the GEMVs, quantizers, fp32 engine) instead of a
+    # scalar load at the start of every wave; C3's GEMV 8.18 -> 8.15 us,
+    # the W8A8 Linear 47.3 -> 46.8 us on MI355X
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
 ]

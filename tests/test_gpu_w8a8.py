@@ -34,7 +34,10 @@ def _x_with_edges(oracle, M, K, seed):
 
 
 @pytest.mark.parametrize("M,K", [(1, 512), (5, 4096), (300, 8192), (7, 48), (3, 1000),
-                                 (2, 8704), (129, 2560), (3, 1024), (5, 3072), (6, 6144)])
+                                 (2, 8704), (129, 2560), (3, 1024), (5, 3072), (6, 6144),
+                                 # large row counts (C4's x among them)
+                                 (2048, 4096), (2047, 4096), (16385, 512), (5101, 1536),
+                                 (1030, 8192), (2050, 3072)])
 def test_quantize_rows_bf16_bit_exact(oracle, dev, M, K):
     """Register paths with 1, 2 and 4 waves per row (K = 512 n), odd row
     counts (a workgroup's last row past M), and the two-pass kernel."""
