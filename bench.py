@@ -67,7 +67,7 @@ def _args():
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c4w8a8,c5,"
-                   "qlinear,bwd,f64,copy,vendor); copy and vendor are run only when named")
+                   "qlinear,bwd,conv2d,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
 
@@ -405,6 +405,33 @@ def bench_backward(steps, warmup):
     return out
 
 
+def bench_conv2d(steps, warmup):
+    """Conv2d.forward (learn/nn/conv.mojo:600-697), fp32 NCHW, on a ResNet-50
+    3 x 3 layer shape: x [32, 64, 56, 56], w [64, 64, 3, 3], stride 1, pad 1,
+    bias; one implicit GEMM per image on the fp32 matrix cores."""
+    import torch
+    import momijo_amd as mj
+    N, C, H, W, OC, k = 32, 64, 56, 56, 64, 3
+    layer = mj.Conv2d(C, OC, (k, k), (1, 1), (1, 1))
+    layer.weight.torch.copy_(_rand_f32((OC, C, k, k), 14, float((2.0 / (C * k * k)) ** 0.5)))
+    layer.bias_t.torch.copy_((torch.rand(OC, device="cuda") - 0.5) / 8)
+    x = mj.Tensor(_rand_f32((N, C, H, W), 15))
+    ms = _time_launches(lambda i: layer.forward(x), steps, warmup)
+    OH, OW = layer.out_size(H, W)
+    flops = 2.0 * N * OC * OH * OW * C * k * k
+    tf = flops / (ms * 1e-3) / 1e12
+    _CPU_INPUTS["conv2d"] = (x.torch[:1].cpu().numpy(), layer.weight.torch.cpu().numpy(),
+                             layer.bias_t.torch.cpu().numpy(), N)
+    return {
+        "name": "conv2d_f32_32x64x56x56_3x3",
+        "metric": "fp32 Conv2d.forward TFLOP/s (NCHW, 3x3, stride 1, pad 1, bias)",
+        "value": tf, "unit": "TFLOP/s", "ms_per_call": ms, "flops_per_call": flops,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_FP32_TFLOPS,
+                     "traffic": _traffic("conv2d_f32_32x64x56x56_3x3")},
+    }
+
+
 def bench_f64(steps, warmup):
     """Float64 matmul (matmul_core_mm / matmul2d) at 2048^3 on fp64 MFMA."""
     import torch
@@ -599,6 +626,25 @@ def cpu_baseline_c5():
             "input_sha256": _sha256(x, Wg, sg, Wu, su, Wd, sd)}
 
 
+def cpu_baseline_conv2d():
+    """Conv2d.forward as the reference computes each output (oracle
+    mo_conv2d_fw_f32: clipped window, strict c, ky, kx order), on the first
+    image of the GPU leg's batch with its weights and bias."""
+    import oracle
+    oracle.build()
+    x, w, b, N = _CPU_INPUTS["conv2d"]
+    per_call, n = _time_cpu(lambda: oracle.conv2d_fw_f32(x, w, b, (1, 1), (1, 1)), 2.0)
+    _, C, H, W = x.shape
+    OC, _, k, _ = w.shape
+    flops = 2.0 * OC * H * W * C * k * k
+    return {"value": flops / per_call / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "ms_per_call": per_call * 1e3, "full_problem_s": per_call * N,
+            "sample": f"image 0 of the GPU leg's batch ({N} images), {n} calls; the full batch "
+                      f"extrapolates linearly to {per_call * N:.1f} s (oracle mo_conv2d_fw_f32, "
+                      "gcc -O2, 1 thread)",
+            "input_sha256": _sha256(x, w, b)}
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -623,7 +669,7 @@ def main():
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
                     ("c4w8a8", bench_c4_w8a8), ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
-                    ("bwd", bench_backward),
+                    ("bwd", bench_backward), ("conv2d", bench_conv2d),
                     ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
         if want(key) and (key not in ("copy", "vendor") or key in only):
             rs = fn(a.steps, a.warmup)
@@ -641,7 +687,7 @@ def main():
             print(f"# cpu baseline done: {cpu['value']:.2e} TFLOP/s", file=sys.stderr, flush=True)
         for key, fn in (("c3", cpu_baseline_c3), ("c3pack", cpu_baseline_c3pack),
                         ("c4", cpu_baseline_c4), ("c5", cpu_baseline_c5),
-                        ("c1", cpu_baseline_c1)):
+                        ("c1", cpu_baseline_c1), ("conv2d", cpu_baseline_conv2d)):
             if key in _CPU_INPUTS:
                 entry = next(r for r in secondary if r["name"].startswith(key + "_"))
                 entry["cpu_baseline"] = fn()

@@ -193,6 +193,31 @@ int32_t mj_launch_linear_bw_db_h(const float *dy, float *db, int64_t N, int64_t 
  * apply_unary, tensor/math.mojo:566-638) and ReLU.forward (layers.mojo:134). */
 int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n, void *stream);
 
+/* ---- conv2d ------------------------------------------------------------- */
+
+/* Conv2d.forward, NCHW fp32 (learn/nn/conv.mojo:600-681, the naive GPU kernel
+ * _gpu_conv2d_fw_kernel, tensor/gpu/runtime.mojo:159-200): x [N,C,H,W],
+ * w [OC,C,kH,kW], b [OC] or NULL, y [N,OC,OH,OW] with
+ * OH = (H + 2 pH - kH) // sH + 1 (floor), OW likewise; zero padding, the
+ * bias after the sum, then `epilogue` (MJ_EPI_NONE for the reference's
+ * layer).  One implicit GEMM per image on fp32 MFMA: y[n] = w [OC, C kH kW]
+ * @ im2col(x[n]), the im2col gathered by the kernel's loader, nothing
+ * materialised.  An empty output (OH or OW <= 0) is MJ_OK with nothing
+ * written.  Padded taps are multiplied as zeros where the reference skips
+ * them: the same sums for finite weights. */
+int32_t mj_conv2d_f32(const float *x, const float *w, const float *b, int32_t epilogue, float *y,
+                      int64_t N, int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
+                      int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW, void *stream);
+
+/* Host-pointer seam of launch_1d_conv2d_fw (tensor/gpu/runtime.mojo:376-470):
+ * the same arguments (OH, OW as the caller computed them, checked against
+ * the geometry: MJ_ERR_SHAPE if they disagree), copy in, mj_conv2d_f32,
+ * copy out into y; has_bias = 0 ignores b. */
+int32_t mj_launch_conv2d_fw_h(const float *x, const float *w, const float *b, float *y, int64_t N,
+                              int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t OC,
+                              int64_t kH, int64_t kW, int64_t sH, int64_t sW, int64_t pH,
+                              int64_t pW, int32_t has_bias);
+
 /* y = x >= s ? x : s over n fp32 elements (may alias): -0 stays -0 at s = 0,
  * NaN gives s.  Replaces Tensor[Float32].maximum_scalar(s) =
  * where_f32(ge_t(self, s), self, s) (tensor/tensor.mojo:4232), which

@@ -11,7 +11,7 @@ from ._lib import (EPI_GELU_TANH, EPI_GELU_TANH_APPROX, EPI_NONE, EPI_RELU, EPI_
                    EPI_SILU, EPI_SILU_APPROX, ROUND_LEGACY, ROUND_RHE, MomijoHipError)
 from .tensor import (Tensor, empty_f32, empty_f64, gemm_bf16_nt, gpu_available, matmul, matmul2d,
                      matmul_backward, tensordot)
-from .nn import (Linear, QuantLinear, ReLU, W8A8Linear, W8Linear, W8MLP, quantize_rowwise_int8,
+from .nn import (Conv2d, Linear, QuantLinear, ReLU, W8A8Linear, W8Linear, W8MLP, quantize_rowwise_int8,
                  quantize_rows_bf16_int8)
 from . import autograd, seam, weights
 from .autograd import GradContext, GradTensor
@@ -22,7 +22,7 @@ __all__ = [
     "Tensor", "matmul", "matmul2d", "matmul_backward", "tensordot", "empty_f32", "empty_f64",
     "gemm_bf16_nt",
     "gpu_available",
-    "Linear", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP", "quantize_rowwise_int8",
+    "Linear", "Conv2d", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP", "quantize_rowwise_int8",
     "quantize_rows_bf16_int8",
     "quantize_symmetric_int8", "matmul_i8_i8_to_i32", "dequantize_i32_to_f32_add_bias",
     "dequantize_i32_scaled",

@@ -60,6 +60,8 @@ SIGNATURES = {
     "mj_matmul_backward_f64": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P]),
     "mj_matmul_backward_f32": (_I32, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P]),
     "mj_activation_f32": (_I32, [_I32, _P, _P, _I64, _P]),
+    "mj_conv2d_f32": (_I32, [_P, _P, _P, _I32, _P] + [_I64] * 11 + [_P]),
+    "mj_launch_conv2d_fw_h": (_I32, [_P, _P, _P, _P] + [_I64] * 13 + [_I32]),
     "mj_maximum_scalar_f32": (_I32, [_P, _F, _P, _I64, _P]),
     "mj_cast_i64_f32": (_I32, [_P, _P, _I64, _P]),
     "mj_gemm_bf16_nt": (_I32, [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I32, _P, _I64, _P]),

@@ -154,6 +154,14 @@ class WorkspaceLease {
   std::unique_lock<std::mutex> lock_;
 };
 
+// Output extent of Conv2d.forward: (size + 2 pad - k) // stride + 1 with
+// floor division (learn/nn/conv.mojo:496-497); <= 0 means an empty output.
+int64_t conv_out(int64_t size, int64_t k, int64_t stride, int64_t pad) {
+  const int64_t num = size + 2 * pad - k;
+  const int64_t q = num >= 0 ? num / stride : -((-num + stride - 1) / stride);
+  return q + 1;
+}
+
 // Launches a planned NT GEMM; `part` is the fp32 workspace when the plan
 // splits K.
 int32_t launch_planned(mj::GemmNT p, const mj::GemmPlan &plan, void *part, hipStream_t stream,
@@ -427,6 +435,32 @@ int32_t mj_launch_linear_bw_db_h(const float *dy, float *db, int64_t N, int64_t 
   });
 }
 
+int32_t mj_launch_conv2d_fw_h(const float *x, const float *w, const float *b, float *y, int64_t N,
+                              int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t OC,
+                              int64_t kH, int64_t kW, int64_t sH, int64_t sW, int64_t pH,
+                              int64_t pW, int32_t has_bias) {
+  if (N < 0 || C < 0 || H < 0 || W < 0 || OC < 0 || kH < 1 || kW < 1 || sH < 1 || sW < 1 ||
+      pH < 0 || pW < 0)
+    return fail(MJ_ERR_ARG, "conv2d: negative size, or kernel / stride below 1");
+  // the seam returns at once when there is nothing to compute
+  // (tensor/gpu/runtime.mojo:398-400)
+  if (N * OC * OH * OW <= 0 || OH <= 0 || OW <= 0) return MJ_OK;
+  if (OH != conv_out(H, kH, sH, pH) || OW != conv_out(W, kW, sW, pW))
+    return fail(MJ_ERR_SHAPE, "conv2d: OH x OW = %lld x %lld, the geometry gives %lld x %lld",
+                (long long)OH, (long long)OW, (long long)conv_out(H, kH, sH, pH),
+                (long long)conv_out(W, kW, sW, pW));
+  if (!y || !w || (C > 0 && !x) || (has_bias && !b)) return fail(MJ_ERR_ARG, "null operand");
+  HostArg a[4] = {{x, nullptr, (size_t)(N * C * H * W) * 4},
+                  {w, nullptr, (size_t)(OC * C * kH * kW) * 4},
+                  {has_bias ? b : nullptr, nullptr, has_bias ? (size_t)OC * 4 : 0},
+                  {nullptr, y, (size_t)(N * OC * OH * OW) * 4}};
+  return with_device_copies(a, 4, [&](void **d) {
+    return mj_conv2d_f32((const float *)d[0], (const float *)d[1],
+                         has_bias ? (const float *)d[2] : nullptr, MJ_EPI_NONE, (float *)d[3], N,
+                         C, H, W, OC, kH, kW, sH, sW, pH, pW, nullptr);
+  });
+}
+
 int32_t mj_matmul_backward_f64(int64_t M, int64_t N, int64_t K, const double *A, const double *B,
                                const double *G, double *dA, double *dB, int32_t accumulate,
                                void *stream) {
@@ -482,6 +516,27 @@ int32_t mj_activation_f32(int32_t epilogue, const float *x, float *y, int64_t n,
   if (n == 0) return MJ_OK;
   if (!x || !y) return fail(MJ_ERR_ARG, "null operand");
   return hip_status(mj::launch_activation_f32(epilogue, x, y, n, S(stream)), "activation launch");
+}
+
+int32_t mj_conv2d_f32(const float *x, const float *w, const float *b, int32_t epilogue, float *y,
+                      int64_t N, int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
+                      int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW,
+                      void *stream) {
+  if (!valid_epi(epilogue)) return fail(MJ_ERR_ARG, "unknown epilogue %d", epilogue);
+  if (N < 0 || C < 0 || H < 0 || W < 0 || OC < 0 || kH < 1 || kW < 1 || sH < 1 || sW < 1 ||
+      pH < 0 || pW < 0)
+    return fail(MJ_ERR_ARG, "conv2d: negative size, or kernel / stride below 1");
+  const int64_t OH = conv_out(H, kH, sH, pH), OW = conv_out(W, kW, sW, pW);
+  if (N == 0 || OC == 0 || OH <= 0 || OW <= 0) return MJ_OK;
+  // every index the kernel forms stays in 32 bits within an image / tile
+  const int64_t lim = (int64_t)1 << 31;
+  if (C * H * W >= lim || OC * C * kH * kW >= lim || OC * OH * OW >= lim || H + 2 * pH >= lim ||
+      W + 2 * pW >= lim || N >= lim)
+    return fail(MJ_ERR_UNSUPPORTED, "conv2d: a dimension product exceeds 2^31");
+  if (!y || !w || (C > 0 && !x)) return fail(MJ_ERR_ARG, "null operand");
+  return hip_status(mj::launch_conv2d_f32(x, w, b, y, N, C, H, W, OC, kH, kW, sH, sW, pH, pW, OH,
+                                          OW, epilogue, S(stream)),
+                    "conv2d launch");
 }
 
 int32_t mj_maximum_scalar_f32(const float *x, float s, float *y, int64_t n, void *stream) {

@@ -43,18 +43,31 @@ template <> struct Acc<double> {
   static __device__ __forceinline__ int row(int lane, int r) { return 4 * r + (lane >> 4); }
 };
 
+// Implicit-GEMM view of an NCHW conv2d (the CONV instantiations): B[k][p] of
+// a batch (image) is x[c][iy][ix] with k = (c kH + ky) kW + kx (the flattened
+// weight index of w[oc][c][ky][kx]), p = oy OW + ox, iy = oy sH - pH + ky,
+// ix = ox sW - pW + kx, and zero where (iy, ix) lies outside the H x W image;
+// the bias is per output row (channel).  One K stage of BK advances (c, ky,
+// kx) by (dc, dky, dkx) with BK = (dc kH + dky) kW + dkx.
+struct ConvDesc {
+  int H = 0, W = 0, OW = 0, kH = 1, kW = 1, sH = 1, sW = 1, pH = 0, pW = 0;
+  int dc = 0, dky = 0, dkx = 0;
+};
+
 // One (batch, 64 x 64 tile) per workgroup: C[b] = epi(A[b] @ B[b] + bias),
 // or with accum set C[b] = C[b] + A[b] @ B[b] (gradient accumulation: the old
 // value plus the finished product, one rounding).
 // The batch index (batch0 + blockIdx.y) is decomposed over up to 5 broadcast
 // batch dimensions into element offsets of A and B; C is contiguous per batch.
-template <typename T, int TB, int BK = kFBK>
+// CONV: B is the image gathered by cv (above) instead of a strided view.
+template <typename T, int TB, int BK = kFBK, bool CONV = false>
 __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const T *__restrict__ A,
                                                       int64_t sAm, int64_t sAk,
                                                       const T *__restrict__ B, int64_t sBk,
                                                       int64_t sBn, const T *__restrict__ bias,
                                                       int epi, int accum, T *__restrict__ C,
-                                                      int64_t ldc, BatchDesc bd, int64_t batch0) {
+                                                      int64_t ldc, BatchDesc bd, int64_t batch0,
+                                                      ConvDesc cv) {
   constexpr int kFBM = TB, kFBN = TB;
   constexpr int NB = TB / 32;        // 16 x 16 blocks per wave and dimension (waves 2 x 2)
   constexpr int EPT = TB * BK / 256; // elements of each operand per thread per stage
@@ -87,7 +100,28 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   const int n0 = (blockIdx.x % tiles_n) * kFBN;
 
   const bool a_k_fast = (sAk == 1);
-  const bool b_n_fast = (sBn == 1) || (sBk != 1);
+  const bool b_n_fast = CONV || (sBn == 1) || (sBk != 1);
+
+  // CONV: a thread's output pixel p = n0 + tid % TB is fixed; element i of
+  // its B loads walks k = k0 + tid / TB + MF i, kept as (c, ky, kx) and
+  // advanced by one stage after each load
+  int cy0 = 0, cx0 = 0, cc[EPT], cky[EPT], ckx[EPT];
+  bool cp_ok = false;
+  if constexpr (CONV) {
+    const int pix = n0 + tid % TB;
+    cp_ok = pix < N;
+    const int oy = cp_ok ? pix / cv.OW : 0;
+    cy0 = oy * cv.sH - cv.pH;
+    cx0 = (pix - oy * cv.OW) * cv.sW - cv.pW;
+    const int khw = cv.kH * cv.kW;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int k = tid / TB + MF * i;
+      cc[i] = k / khw;
+      cky[i] = (k - cc[i] * khw) / cv.kW;
+      ckx[i] = k - cc[i] * khw - cky[i] * cv.kW;
+    }
+  }
 
   T ra[EPT], rb[EPT];
   auto load = [&](int k0) {
@@ -101,11 +135,26 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
     }
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      int n, k;
-      if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
-      else          { k = tid % BK; n = tid / BK + KF * i; }
-      const int gn = n0 + n, gk = k0 + k;
-      rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : T(0);
+      if constexpr (CONV) {
+        const int iy = cy0 + cky[i], ix = cx0 + ckx[i];
+        const bool in = cp_ok && k0 + tid / TB + MF * i < K && (unsigned)iy < (unsigned)cv.H &&
+                        (unsigned)ix < (unsigned)cv.W;
+        rb[i] = in ? B[((int64_t)cc[i] * cv.H + iy) * cv.W + ix] : T(0);
+        // advance (c, ky, kx) by BK: each digit carries at most once
+        ckx[i] += cv.dkx;
+        const int cx = ckx[i] >= cv.kW;
+        ckx[i] -= cx ? cv.kW : 0;
+        cky[i] += cv.dky + cx;
+        const int cyc = cky[i] >= cv.kH;
+        cky[i] -= cyc ? cv.kH : 0;
+        cc[i] += cv.dc + cyc;
+      } else {
+        int n, k;
+        if (b_n_fast) { n = tid % TB; k = tid / TB + MF * i; }
+        else          { k = tid % BK; n = tid / BK + KF * i; }
+        const int gn = n0 + n, gk = k0 + k;
+        rb[i] = (gn < N && gk < K) ? B[(int64_t)gk * sBk + (int64_t)gn * sBn] : T(0);
+      }
     }
   };
   auto store = [&](int buf) {
@@ -161,7 +210,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
   for (int j = 0; j < NB; ++j) {
     const int n = n0 + wn * (TB / 2) + j * 16 + (lane & 15);
     if (n >= N) continue;
-    const T bb = bias ? bias[n] : T(0);
+    const T bb = (bias && !CONV) ? bias[n] : T(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -171,7 +220,7 @@ __global__ __launch_bounds__(256) void gemm_fx_kernel(int M, int N, int K, const
           T v = acc[i][j][r];
           if (bias) {
 #pragma clang fp contract(off)
-            v = v + bb;
+            v = v + (CONV ? bias[m] : bb);
           }
           if constexpr (sizeof(T) == sizeof(float)) v = apply_epi(epi, v);  // fp64: none
           T *dst = C + (int64_t)m * ldc + n;
@@ -313,15 +362,15 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
     if (big)
       hipLaunchKernelGGL((gemm_fx_kernel<T, 128>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0);
+                         ldc, bd, b0, ConvDesc{});
     else if (tiny)
       hipLaunchKernelGGL((gemm_fx_kernel<T, 32, kTinyBK<T>>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0);
+                         ldc, bd, b0, ConvDesc{});
     else
       hipLaunchKernelGGL((gemm_fx_kernel<T, 64>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
                          (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0);
+                         ldc, bd, b0, ConvDesc{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -356,6 +405,56 @@ hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int
                            int64_t ldc, int accum, hipStream_t stream) {
   return launch_fx<double>(M, N, K, A, sAm, sAk, B, sBk, sBn, nullptr, 0, accum, C, ldc,
                            BatchDesc{}, 1, stream);
+}
+
+// Conv2d.forward (NCHW) as one implicit GEMM per image: y[n] [OC, OH OW] =
+// w [OC, C kH kW] @ im2col(x[n]) [C kH kW, OH OW] + b[oc], the image index
+// on the grid's second dimension.  Tiles as the matmul picks them (64 x 64,
+// 128 x 128 for large problems, 32 x 32 for tiny ones).
+hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, float *y, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
+                             int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW,
+                             int64_t OH, int64_t OW, int epi, hipStream_t stream) {
+  const int64_t M = OC, Ng = OH * OW, K = C * kH * kW;
+  BatchDesc bd;
+  bd.rank = 1;
+  bd.shape[0] = N;
+  bd.a_stride[0] = 0;
+  bd.b_stride[0] = C * H * W;
+  const int64_t tiles128 = ((M + 127) / 128) * ((Ng + 127) / 128);
+  const bool big = M >= 256 && Ng >= 256 && tiles128 * N >= 512;
+  const bool tiny = !big && ((M + 63) / 64) * ((Ng + 63) / 64) * N < 64;
+  const int TBs = big ? 128 : (tiny ? 32 : 64);
+  const int BKs = tiny ? kTinyBK<float> : kFBK;
+  ConvDesc cv;
+  cv.H = (int)H; cv.W = (int)W; cv.OW = (int)OW; cv.kH = (int)kH; cv.kW = (int)kW;
+  cv.sH = (int)sH; cv.sW = (int)sW; cv.pH = (int)pH; cv.pW = (int)pW;
+  cv.dc = (int)(BKs / (kH * kW));
+  cv.dky = (int)((BKs % (kH * kW)) / kW);
+  cv.dkx = (int)(BKs % kW);
+  const int64_t tiles64 = ((M + TBs - 1) / TBs) * ((Ng + TBs - 1) / TBs);
+  if (tiles64 > INT32_MAX) return hipErrorInvalidValue;
+  const int tiles = (int)tiles64;
+  constexpr int64_t kMaxGridY = 65535;
+  for (int64_t b0 = 0; b0 < N; b0 += kMaxGridY) {
+    const int64_t nb = N - b0 < kMaxGridY ? N - b0 : kMaxGridY;
+    if (big)
+      hipLaunchKernelGGL((gemm_fx_kernel<float, 128, kFBK, true>), dim3(tiles, (unsigned)nb),
+                         dim3(256), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
+                         (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0, cv);
+    else if (tiny)
+      hipLaunchKernelGGL((gemm_fx_kernel<float, 32, kTinyBK<float>, true>),
+                         dim3(tiles, (unsigned)nb), dim3(256), 0, stream, (int)M, (int)Ng, (int)K,
+                         w, K, (int64_t)1, x, (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0,
+                         cv);
+    else
+      hipLaunchKernelGGL((gemm_fx_kernel<float, 64, kFBK, true>), dim3(tiles, (unsigned)nb),
+                         dim3(256), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
+                         (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0, cv);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // Column sums s[o] = sum_n X[n, o] of a row-major [N, OutF] matrix, in

@@ -89,6 +89,13 @@ hipError_t launch_matvec_f32(int64_t M, int64_t N, const float *A, int64_t sAm, 
                              const float *x, int64_t sx, float *y, hipStream_t stream);
 hipError_t launch_activation_f32(int epi, const float *x, float *y, int64_t n,
                                  hipStream_t stream);
+// Conv2d.forward, NCHW fp32, as an implicit GEMM per image (gemm_f32.hip):
+// x [N,C,H,W], w [OC,C,kH,kW], b [OC] or null, y [N,OC,OH,OW]; OH, OW from
+// the caller (>= 1); C H W, OC C kH kW and OC OH OW below 2^31.
+hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, float *y, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
+                             int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW,
+                             int64_t OH, int64_t OW, int epi, hipStream_t stream);
 // y = x >= s ? x : s elementwise (Tensor[Float32].maximum_scalar).
 hipError_t launch_maximum_scalar_f32(const float *x, float s, float *y, int64_t n,
                                      hipStream_t stream);

@@ -87,6 +87,79 @@ class Linear:
     backward_gpu = backward
 
 
+class Conv2d:
+    """Conv2d(in_channels, out_channels, kernel, stride, pad, bias)
+    (learn/nn/conv.mojo:443-476): weight [OC, C, kH, kW] fp32, bias_t [OC].
+
+    ``forward`` is Conv2d.forward / forward_auto / forward_gpu
+    (:494-597, 600-697): NCHW, zero padding, OH = (H + 2 pH - kH) // sH + 1,
+    the bias added after the sum, computed as one implicit GEMM per image
+    on the fp32 matrix cores (``mj_conv2d_f32``).  The weights are
+    initialised as the reference does in distribution (He normal,
+    N(0, 1) * sqrt(2 / fan_in), bias zero), from torch's device generator:
+    the reference's global RNG stream is not reproduced; callers that need
+    given weights assign ``weight`` / ``bias_t``.  An input whose channel
+    count differs from the weight's is refused (the reference would read
+    past the weight)."""
+
+    def __init__(self, in_channels: int, out_channels: int, kernel, stride=(1, 1),
+                 pad=(0, 0), bias: bool = True):
+        kH, kW = kernel
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_h, self.kernel_w = int(kH), int(kW)
+        self.stride_h, self.stride_w = (int(v) for v in stride)
+        self.pad_h, self.pad_w = (int(v) for v in pad)
+        if min(self.kernel_h, self.kernel_w, self.stride_h, self.stride_w) < 1 or \
+                min(self.pad_h, self.pad_w) < 0:
+            raise ValueError("kernel and stride must be >= 1, padding >= 0")
+        self.bias = bias
+        fan_in = in_channels * self.kernel_h * self.kernel_w
+        dev = _device()
+        w = torch.randn((out_channels, in_channels, self.kernel_h, self.kernel_w),
+                        dtype=torch.float32, device=dev)
+        self.weight = Tensor(w * np.float32(np.sqrt(2.0 / max(fan_in, 1))))
+        self.bias_t = Tensor(torch.zeros((out_channels if bias else 0,), dtype=torch.float32,
+                                         device=dev))
+
+    def out_size(self, H: int, W: int) -> tuple[int, int]:
+        """(OH, OW) with floor division (conv.mojo:496-497)."""
+        return ((H + 2 * self.pad_h - self.kernel_h) // self.stride_h + 1,
+                (W + 2 * self.pad_w - self.kernel_w) // self.stride_w + 1)
+
+    def forward_act(self, x: Tensor, epi: int) -> Tensor:
+        xt = x.torch
+        if xt.dim() != 4 or xt.shape[1] != self.in_channels:
+            raise ValueError(f"Conv2d({self.in_channels}, ...) takes [N, {self.in_channels}, H, W], "
+                             f"got {list(xt.shape)}")
+        if xt.dtype != torch.float32:
+            raise TypeError("Conv2d takes Float32 inputs")
+        xt = xt.contiguous()
+        N, C, H, W = xt.shape
+        OH, OW = self.out_size(H, W)
+        w = self.weight.torch.contiguous()
+        if tuple(w.shape) != (self.out_channels, C, self.kernel_h, self.kernel_w):
+            raise ValueError(f"weight must be [{self.out_channels}, {C}, {self.kernel_h}, "
+                             f"{self.kernel_w}], got {list(w.shape)}")
+        y = torch.empty((N, self.out_channels, max(OH, 0), max(OW, 0)), dtype=torch.float32,
+                        device=xt.device)
+        if y.numel() == 0:
+            return Tensor(y)
+        b = self.bias_t.torch
+        bptr = _ptr(b) if self.bias and b.numel() == self.out_channels else None
+        _lib.call("mj_conv2d_f32", _ptr(xt), _ptr(w), bptr, epi, _ptr(y), N, C, H, W,
+                  self.out_channels, self.kernel_h, self.kernel_w, self.stride_h, self.stride_w,
+                  self.pad_h, self.pad_w, _stream())
+        return Tensor(y)
+
+    def forward(self, x: Tensor) -> Tensor:
+        """Conv2d.forward -> forward_auto (conv.mojo:697-708)."""
+        return self.forward_act(x, _lib.EPI_NONE)
+
+    forward_auto = forward
+    forward_gpu = forward
+
+
 class ReLU:
     """ReLU.forward = layers.mojo's own _maximum_scalar(x, 0): v > 0 ? v : 0
     (layers.mojo:117-137), so -0 and NaN give +0 -- unlike
@@ -282,5 +355,5 @@ def quantize_rows_bf16_int8(x: torch.Tensor):
     return xq, sx
 
 
-__all__ = ["Linear", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP",
+__all__ = ["Linear", "Conv2d", "ReLU", "QuantLinear", "W8Linear", "W8A8Linear", "W8MLP",
            "quantize_rowwise_int8", "quantize_rows_bf16_int8", "_device"]

@@ -1,6 +1,7 @@
 """The reference's device seam on this backend: ``launch_1d_linear_fw`` and
-its backward siblings (tensor/gpu/runtime.mojo:504-903) with their exact
-argument lists and their contract.
+its backward siblings (tensor/gpu/runtime.mojo:504-903), and
+``launch_1d_conv2d_fw`` (:360-470), with their exact argument lists and
+their contract.
 
 The reference launchers take host buffers (``List[Float32]``), the number of
 logical threads, a block size and a ``kernel`` -- a CPU function of the
@@ -37,6 +38,9 @@ Kernel1D_LinearBW_DX = Callable[..., None]
 Kernel1D_LinearBW_DW = Callable[..., None]
 # Kernel1D_LinearBW_DB (runtime.mojo:530-535): kernel(tid, dy, db, N, OutF)
 Kernel1D_LinearBW_DB = Callable[..., None]
+# Kernel1D_Conv2DFW (runtime.mojo:360-374): kernel(tid, x, w, b, y, N, C, H, W, OH, OW, OC,
+# kH, kW, sH, sW, pH, pW, has_bias)
+Kernel1D_Conv2DFW = Callable[..., None]
 
 
 def gpu_available() -> bool:
@@ -170,6 +174,31 @@ def launch_1d_linear_bw_db(total_threads: int, block_size: int, kernel: Kernel1D
     return "cpu"
 
 
+def launch_1d_conv2d_fw(total_threads: int, block_size: int, kernel: Kernel1D_Conv2DFW,
+                        x, w, b, y: np.ndarray, N: int, C: int, H: int, W: int, OH: int,
+                        OW: int, OC: int, kH: int, kW: int, sH: int, sW: int, pH: int, pW: int,
+                        has_bias: bool, *, strict: bool = False) -> str:
+    """launch_1d_conv2d_fw (runtime.mojo:376-470): y [N,OC,OH,OW] = conv2d of
+    x [N,C,H,W] with w [OC,C,kH,kW] (+ b[oc] when has_bias), NCHW, zero
+    padding.  Nothing to compute (N OC OH OW <= 0) returns at once, as the
+    reference's GPU path does (:398-400)."""
+    total = N * OC * OH * OW
+    if total <= 0 and gpu_available():
+        return "gpu"
+    hx = _host_in(x, N * C * H * W, "x")
+    hw = _host_in(w, OC * C * kH * kW, "w")
+    hb = _host_in(b, OC, "b") if has_bias else None
+    hy = _host_out(y, max(total, 0), "y")
+    if _device_call("mj_launch_conv2d_fw_h", strict, _ptr(hx), _ptr(hw), _ptr(hb), _ptr(hy), N,
+                    C, H, W, OH, OW, OC, kH, kW, sH, sW, pH, pW, int(bool(has_bias))):
+        return "gpu"
+    _cpu_fallback(total_threads, block_size,
+                  lambda tid: kernel(tid, x, w, b, y, N, C, H, W, OH, OW, OC, kH, kW, sH, sW,
+                                     pH, pW, has_bias))
+    return "cpu"
+
+
 __all__ = ["gpu_available", "launch_1d_linear_fw", "launch_1d_linear_bw_dx",
-           "launch_1d_linear_bw_dw", "launch_1d_linear_bw_db", "Kernel1D_LinearFW",
-           "Kernel1D_LinearBW_DX", "Kernel1D_LinearBW_DW", "Kernel1D_LinearBW_DB"]
+           "launch_1d_linear_bw_dw", "launch_1d_linear_bw_db", "launch_1d_conv2d_fw",
+           "Kernel1D_LinearFW", "Kernel1D_LinearBW_DX", "Kernel1D_LinearBW_DW",
+           "Kernel1D_LinearBW_DB", "Kernel1D_Conv2DFW"]

@@ -21,6 +21,11 @@ Parity status of each restated function (how it is pinned, see
   double.  The Mojo stdlib ``exp`` ulp behaviour is **parity unpinned**.
 * maximum_scalar_f32: the -0 / NaN / equal-to-s cases against the mask rule
   x >= s written out, plus numpy's fmax away from those cases.
+* conv2d_fw_f32: integer-valued inputs whose sums are exact (against an int64
+  restatement with explicit zero padding), the 1 x 1 / stride-1 case against
+  the pinned matmul, delta kernels (shifted copies of x, padding zeros),
+  valid-tap clipping against the strict-order float32 loop written out, and
+  torch's CPU conv2d within the fp32 summation bound.
 * astype_f32_from_int: integers above 2^24 with exact ties (2^24 + 1 -> 2^24,
   2^24 + 3 -> 2^24 + 4), 2^63 - 1, negatives, and numpy's int64 -> float32
   cast (round to nearest even) on random 64-bit integers.
@@ -117,6 +122,7 @@ def _declare(L):
         "mo_linear_backward_f32": (None, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
         "mo_matmul_backward_f64": (None, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
         "mo_matmul_backward_f32": (None, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
+        "mo_conv2d_fw_f32": (None, [_P, _P, _P, _P] + [_I64] * 15),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -530,3 +536,30 @@ def mlp_w8a16(x_bf16, Wg, sg, Wu, su, Wd, sd, rows=None):
     lib().mo_mlp_w8a16(_ptr(x), _ptr(Wg), _ptr(sg), _ptr(Wu), _ptr(su), _ptr(Wd), _ptr(sd),
                        _ptr(h), _ptr(y), K, I, H, m0, m1, _ptr(scratch))
     return h, y
+
+
+# ----------------------------------------------------------------- conv2d
+def conv_out_size(size: int, k: int, s: int, p: int) -> int:
+    """(size + 2 p - k) // s + 1 with floor division, as Conv2d.forward sizes
+    its output (learn/nn/conv.mojo:496-497, 682-683)."""
+    return (size + 2 * p - k) // s + 1
+
+
+def conv2d_fw_f32(x, w, b=None, stride=(1, 1), pad=(0, 0), images=None) -> np.ndarray:
+    """Conv2d.forward (NCHW, learn/nn/conv.mojo:600-681).  images=(n0, n1)
+    limits the computed images; returns y [n1 - n0, OC, OH, OW]."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    N, C, H, W = x.shape
+    OC, C2, kH, kW = w.shape
+    assert C == C2, "x and w disagree on the input channels"
+    sH, sW = stride
+    pH, pW = pad
+    OH, OW = conv_out_size(H, kH, sH, pH), conv_out_size(W, kW, sW, pW)
+    n0, n1 = images if images is not None else (0, N)
+    bb = None if b is None else _c(b, np.float32)
+    y = np.empty((n1 - n0, OC, max(OH, 0), max(OW, 0)), np.float32)
+    if OH > 0 and OW > 0:
+        lib().mo_conv2d_fw_f32(_ptr(x), _ptr(w), _ptr(bb), _ptr(y), N, C, H, W, OC, kH, kW,
+                               sH, sW, pH, pW, OH, OW, n0, n1)
+    return y

@@ -765,3 +765,48 @@ MO_API void mo_matmul_backward_f32(const float *a, const float *b, const float *
                 db[k * N + j] = accumulate ? db[k * N + j] + acc : acc;
             }
 }
+
+/* ------------------------------------------------------------------------ */
+/* conv2d                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Conv2d.forward, NCHW, as Conv2d._kernel_conv2d_fwd computes each output
+ * (learn/nn/conv.mojo:600-681; the same arithmetic as forward_cpu_parallel,
+ * :494-597, and the GPU kernel _gpu_conv2d_fw_kernel,
+ * tensor/gpu/runtime.mojo:159-200): for output (n, oc, oy, ox) the window
+ * is clipped to the input (ky in [ky_start, ky_end), kx likewise: padded taps
+ * are skipped, not multiplied by zero), sum = 0 then sum = sum + x * w over
+ * ic, ky, kx in ascending order (one rounding per multiply and per add), and
+ * the bias is added after the sum.  x [N,C,H,W], w [OC,C,kH,kW], b [OC] or
+ * NULL, y [N,OC,OH,OW]; images n0 .. n1 - 1 only (y indexed from image n0). */
+MO_API void mo_conv2d_fw_f32(const float *x, const float *w, const float *b, float *y, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
+                             int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW,
+                             int64_t OH, int64_t OW, int64_t n0, int64_t n1) {
+    (void)N;
+    const int64_t HW = H * W, CHW = C * HW, kHW = kH * kW, CkHW = C * kHW;
+    for (int64_t n = n0; n < n1; ++n)
+        for (int64_t oc = 0; oc < OC; ++oc)
+            for (int64_t oy = 0; oy < OH; ++oy) {
+                const int64_t iy0 = oy * sH - pH;
+                const int64_t ky_start = iy0 < 0 ? -iy0 : 0;
+                int64_t ky_end = kH;
+                if (iy0 + kH > H) ky_end = kH - (iy0 + kH - H);
+                for (int64_t ox = 0; ox < OW; ++ox) {
+                    const int64_t ix0 = ox * sW - pW;
+                    const int64_t kx_start = ix0 < 0 ? -ix0 : 0;
+                    int64_t kx_end = kW;
+                    if (ix0 + kW > W) kx_end = kW - (ix0 + kW - W);
+                    float sum = 0.0f;
+                    for (int64_t ic = 0; ic < C; ++ic)
+                        for (int64_t ky = ky_start; ky < ky_end; ++ky)
+                            for (int64_t kx = kx_start; kx < kx_end; ++kx) {
+                                const float xv = x[n * CHW + ic * HW + (iy0 + ky) * W + ix0 + kx];
+                                const float wv = w[oc * CkHW + ic * kHW + ky * kW + kx];
+                                sum = sum + xv * wv;
+                            }
+                    if (b) sum = sum + b[oc];
+                    y[(((n - n0) * OC + oc) * OH + oy) * OW + ox] = sum;
+                }
+            }
+}

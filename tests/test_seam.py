@@ -59,6 +59,28 @@ def k_bw_db(tid, dy, db, N, OutF):
     db[tid] = acc
 
 
+def k_conv2d_fw(tid, x, w, b, y, N, C, H, W, OH, OW, OC, kH, kW, sH, sW, pH, pW, has_bias):
+    """The reference's _kernel_conv2d_fwd (learn/nn/conv.mojo:600-681)."""
+    if tid >= N * OC * OH * OW:
+        return
+    n, r = divmod(tid, OC * OH * OW)
+    oc, r = divmod(r, OH * OW)
+    oy, ox = divmod(r, OW)
+    iy0, ix0 = oy * sH - pH, ox * sW - pW
+    ky0, ky1 = max(0, -iy0), kH - max(0, iy0 + kH - H)
+    kx0, kx1 = max(0, -ix0), kW - max(0, ix0 + kW - W)
+    acc = f32(0)
+    for ic in range(C):
+        for ky in range(ky0, ky1):
+            for kx in range(kx0, kx1):
+                xv = f32(x[((n * C + ic) * H + iy0 + ky) * W + ix0 + kx])
+                wv = f32(w[((oc * C + ic) * kH + ky) * kW + kx])
+                acc = f32(acc + f32(xv * wv))
+    if has_bias:
+        acc = f32(acc + f32(b[oc]))
+    y[tid] = acc
+
+
 class _FailingLib:
     """Stands in for the loaded library: a device is reported, and every
     host-pointer launch returns MJ_ERR_DEVICE."""
@@ -168,3 +190,22 @@ def test_output_buffer_must_be_writable_float32(mode):
         seam.launch_1d_linear_fw(4, 4, k_linear_fw, z, z, z, [0.0] * 4, 2, 2, 2, False)
     with pytest.raises(ValueError):
         seam.launch_1d_linear_fw(4, 4, k_linear_fw, z[:3], z, z, z.copy(), 2, 2, 2, False)
+
+
+def test_conv2d_fw_falls_back_to_kernel(oracle, mode):
+    N, C, H, W, OC, kH, kW, sH, sW, pH, pW = 2, 3, 6, 5, 4, 3, 3, 2, 1, 1, 1
+    x = oracle.randn_f32((N, C, H, W), seed=31)
+    w = oracle.randn_f32((OC, C, kH, kW), seed=32)
+    b = oracle.randu_f32((OC,), -1 / 16, 1 / 16, seed=33)
+    OH, OW = oracle.conv_out_size(H, kH, sH, pH), oracle.conv_out_size(W, kW, sW, pW)
+    y = np.zeros(N * OC * OH * OW, np.float32)
+    seen = []
+    path = seam.launch_1d_conv2d_fw(N * OC * OH * OW, 16, _counted(k_conv2d_fw, seen),
+                                    x.reshape(-1), w.reshape(-1), b, y, N, C, H, W, OH, OW, OC,
+                                    kH, kW, sH, sW, pH, pW, True)
+    assert path == "cpu"
+    assert seen == list(range(N * OC * OH * OW))
+    np.testing.assert_array_equal(y.reshape(N, OC, OH, OW),
+                                  oracle.conv2d_fw_f32(x, w, b, (sH, sW), (pH, pW)))
+    if mode is not None:
+        assert mode.calls == ["mj_launch_conv2d_fw_h"]
