@@ -15,6 +15,8 @@
 // whichever dimension has unit stride with consecutive lanes so global reads
 // stay coalesced.  A grid dimension over broadcast batch indices serves
 // tensordot's batched paths.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -407,15 +409,211 @@ hipError_t launch_gemm_f64(int64_t M, int64_t N, int64_t K, const double *A, int
                            BatchDesc{}, 1, stream);
 }
 
+// Conv2d.forward with OC >= 64 (conv2d_fx_kernel<NBN>): 64 x TBN tiles of
+// (output channel, output pixel of one image), TBN = 32 NBN, eight waves
+// 4 x 2 of 16 x 16 NBN, 16-deep K stages through LDS, with the MFMA of
+// gemm_fx_kernel in the same k order (k ascending by 4, lane group fk
+// supplying k = 4 t + fk): the outputs are bit-identical to it.
+// The gather: thread t owns pixel n0 + t % 256 of the tile (t % 256 < TBN)
+// and loads 8 k of each stage, waves 0-3 the first 8, waves 4-7 the last 8.
+// Element k = (c kH + ky) kW + kx sits at (pixel base) + c H W + ky W + kx in
+// the image, pixel base = (oy sH - pH) W + ox sW - pW; the (c, ky, kx) walk
+// is the same for every lane of a wave (scalar registers), and an out-of-range
+// buffer offset (a tap in the padding, k >= K, a pixel past the image) loads
+// zero.  Two stages are in flight in registers while one multiplies from LDS.
+// The LDS rows are padded to 16 mod 32 words, so the fragment reads of four
+// consecutive k rows (16 lanes each) hit distinct banks.  Against one wave
+// per SIMD (four waves of 32 x 16 NBN) the eight waves ran the bench layer
+// (32 x 64 x 56 x 56, 3 x 3, pad 1) 116.5 us against 126.8 (MI355X, same
+// tile).  Needs C H W and OC C kH kW below 2^29 (32-bit byte offsets).
+template <int NBN>
+__global__ __launch_bounds__(512) void conv2d_fx_kernel(int M, int Ng, int K,
+                                                        const float *__restrict__ w,
+                                                        const float *__restrict__ x,
+                                                        const float *__restrict__ bias, int epi,
+                                                        float *__restrict__ y, int64_t img0,
+                                                        int C, ConvDesc cv) {
+  constexpr int TBM = 64, TBN = 32 * NBN, BK = 16;
+  constexpr int LDA = TBM + 16, LDB = TBN + 16;
+  __shared__ float As[2][BK][LDA];
+  __shared__ float Bs[2][BK][LDB];
+  const int64_t img = img0 + blockIdx.y;
+  const int hw = cv.H * cv.W;
+  const int64_t chw = (int64_t)C * hw;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + img * chw, chw * 4);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (int64_t)M * K * 4);
+  y += img * (int64_t)M * Ng;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_n = (Ng + TBN - 1) / TBN;
+  const int m0 = (blockIdx.x / tiles_n) * TBM;
+  const int n0 = (blockIdx.x % tiles_n) * TBN;
+
+  const int kg = wave >> 2;      // k group of the B gather (wave-uniform)
+  const int px = tid & 255;
+  int iy0 = -(1 << 28), ix0 = 0, pbase = 0;
+  if (px < TBN && n0 + px < Ng) {
+    const int pix = n0 + px;
+    const int oy = pix / cv.OW;
+    iy0 = oy * cv.sH - cv.pH;
+    ix0 = (pix - oy * cv.OW) * cv.sW - cv.pW;
+    pbase = iy0 * cv.W + ix0;
+  }
+  // walk state: the (c, ky, kx) of k = 8 kg of the next stage to load
+  const int khw = cv.kH * cv.kW;
+  int wc = (8 * kg) / khw;
+  int wky = (8 * kg - wc * khw) / cv.kW;
+  int wkx = 8 * kg - wc * khw - wky * cv.kW;
+  const int ak = tid & 15, am = tid >> 4;
+
+  float ra[2][2], rb[2][8];
+  auto step = [&]() {
+    if (++wkx == cv.kW) {
+      wkx = 0;
+      if (++wky == cv.kH) {
+        wky = 0;
+        ++wc;
+      }
+    }
+  };
+  auto load = [&](int k0, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int m = m0 + am + 32 * i, k = k0 + ak;
+      const uint32_t off = (m < M && k < K) ? (uint32_t)(m * K + k) * 4u : kOobOffset;
+      ra[SL][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int iy = iy0 + wky, ix = ix0 + wkx;
+      const bool in = (unsigned)iy < (unsigned)cv.H && (unsigned)ix < (unsigned)cv.W &&
+                      k0 + 8 * kg + i < K;
+      const uint32_t off = in ? (uint32_t)(pbase + wc * hw + wky * cv.W + wkx) * 4u : kOobOffset;
+      rb[SL][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+      step();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) step();
+  };
+  auto store = [&](int buf, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) As[buf][ak][am + 32 * i] = ra[SL][i];
+    if (px < TBN) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Bs[buf][8 * kg + i][px] = rb[SL][i];
+    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+
+  f32x4 acc[NBN];
+#pragma unroll
+  for (int j = 0; j < NBN; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int nk = (K + BK - 1) / BK;
+  const int fr = lane & 15, fk = lane >> 4;
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+      const float a = As[buf][kk + fk][wm * 16 + fr];
+      float b[NBN];
+#pragma unroll
+      for (int j = 0; j < NBN; ++j) b[j] = Bs[buf][kk + fk][wn * 16 * NBN + j * 16 + fr];
+#pragma unroll
+      for (int j = 0; j < NBN; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[j], acc[j], 0, 0, 0);
+    }
+  };
+  load(0, S0());
+  if (nk > 1) load(BK, S1());
+  store(0, S0());
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    if (kt + 2 < nk) load((kt + 2) * BK, S0());
+    mma(0);
+    store(1, S1());
+    __syncthreads();
+    if (kt + 3 < nk) load((kt + 3) * BK, S1());
+    mma(1);
+    if (kt + 2 < nk) store(0, S0());
+    __syncthreads();
+  }
+  if (kt < nk) mma(0);
+
+#pragma unroll
+  for (int j = 0; j < NBN; ++j) {
+    const int n = n0 + wn * 16 * NBN + j * 16 + fr;
+    if (n >= Ng) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + wm * 16 + 4 * fk + r;
+      if (m < M) {
+        float v = acc[j][r];
+        if (bias) {
+#pragma clang fp contract(off)
+          v = v + bias[m];
+        }
+        y[(int64_t)m * Ng + n] = apply_epi(epi, v);
+      }
+    }
+  }
+}
+
 // Conv2d.forward (NCHW) as one implicit GEMM per image: y[n] [OC, OH OW] =
 // w [OC, C kH kW] @ im2col(x[n]) [C kH kW, OH OW] + b[oc], the image index
-// on the grid's second dimension.  Tiles as the matmul picks them (64 x 64,
-// 128 x 128 for large problems, 32 x 32 for tiny ones).
+// on the grid's second dimension: conv2d_fx_kernel's 64 x 224 or 64 x 256
+// tiles when they apply (below), else the matmul engine's square tiles as
+// the matmul picks them (64 x 64, 128 x 128 for large problems, 32 x 32 for
+// tiny ones).  Both sum each output in the same k order.
 hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, float *y, int64_t N,
                              int64_t C, int64_t H, int64_t W, int64_t OC, int64_t kH,
                              int64_t kW, int64_t sH, int64_t sW, int64_t pH, int64_t pW,
                              int64_t OH, int64_t OW, int epi, hipStream_t stream) {
   const int64_t M = OC, Ng = OH * OW, K = C * kH * kW;
+  constexpr int64_t kMaxGridY = 65535;
+  ConvDesc cv;
+  cv.H = (int)H; cv.W = (int)W; cv.OW = (int)OW; cv.kH = (int)kH; cv.kW = (int)kW;
+  cv.sH = (int)sH; cv.sW = (int)sW; cv.pH = (int)pH; cv.pW = (int)pW;
+  // OC >= 64 and a grid of at least 256 workgroups: conv2d_fx_kernel with
+  // 224- or 256-pixel tiles, whichever leaves fewer pixel columns on the
+  // busiest CU (workgroups of all images dealt over 256 CUs; 256 on a tie).
+  // Narrower tiles of that kernel measured slower than the square tiles
+  // below (128: 158.6 us, against 137 us for 64 x 64 on the bench layer).
+  if (M >= 64 && C * H * W < ((int64_t)1 << 29) && M * K < ((int64_t)1 << 29)) {
+    int nbn = 0;
+    int64_t best = INT64_MAX, wgs_best = 0;
+    for (int c : {8, 7}) {
+      const int64_t tbn = 32 * c;
+      const int64_t wgs = ((M + 63) / 64) * ((Ng + tbn - 1) / tbn) * N;
+      const int64_t cost = (wgs + 255) / 256 * tbn;
+      if (cost < best) {
+        best = cost;
+        nbn = c;
+        wgs_best = wgs;
+      }
+    }
+    if (wgs_best >= 256) {
+      const int64_t tiles_c = ((M + 63) / 64) * ((Ng + 32 * nbn - 1) / (32 * nbn));
+      if (tiles_c > INT32_MAX) return hipErrorInvalidValue;
+      for (int64_t b0 = 0; b0 < N; b0 += kMaxGridY) {
+        const int64_t nb = N - b0 < kMaxGridY ? N - b0 : kMaxGridY;
+        const dim3 g((unsigned)tiles_c, (unsigned)nb);
+        if (nbn == 8)
+          hipLaunchKernelGGL((conv2d_fx_kernel<8>), g, dim3(512), 0, stream, (int)M, (int)Ng,
+                             (int)K, w, x, b, epi, y, b0, (int)C, cv);
+        else
+          hipLaunchKernelGGL((conv2d_fx_kernel<7>), g, dim3(512), 0, stream, (int)M, (int)Ng,
+                             (int)K, w, x, b, epi, y, b0, (int)C, cv);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    }
+  }
   BatchDesc bd;
   bd.rank = 1;
   bd.shape[0] = N;
@@ -426,16 +624,12 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, flo
   const bool tiny = !big && ((M + 63) / 64) * ((Ng + 63) / 64) * N < 64;
   const int TBs = big ? 128 : (tiny ? 32 : 64);
   const int BKs = tiny ? kTinyBK<float> : kFBK;
-  ConvDesc cv;
-  cv.H = (int)H; cv.W = (int)W; cv.OW = (int)OW; cv.kH = (int)kH; cv.kW = (int)kW;
-  cv.sH = (int)sH; cv.sW = (int)sW; cv.pH = (int)pH; cv.pW = (int)pW;
   cv.dc = (int)(BKs / (kH * kW));
   cv.dky = (int)((BKs % (kH * kW)) / kW);
   cv.dkx = (int)(BKs % kW);
   const int64_t tiles64 = ((M + TBs - 1) / TBs) * ((Ng + TBs - 1) / TBs);
   if (tiles64 > INT32_MAX) return hipErrorInvalidValue;
   const int tiles = (int)tiles64;
-  constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < N; b0 += kMaxGridY) {
     const int64_t nb = N - b0 < kMaxGridY ? N - b0 : kMaxGridY;
     if (big)

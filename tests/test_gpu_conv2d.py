@@ -44,6 +44,9 @@ def _conv(dev, x, w, b, stride, pad, epi=mj.EPI_NONE):
     (2, 2, 5, 5, 3, 3, 3, 1, 1, 4, 4),          # windows entirely in the padding
     (1, 6, 4, 9, 7, 4, 9, 1, 1, 0, 0),          # kernel as wide as the input
     (2, 24, 12, 12, 20, 7, 7, 3, 3, 3, 3),      # K = 1176: many K stages, carries of every digit
+    (3, 5, 33, 47, 70, 5, 3, 2, 1, 2, 1),       # ragged channel and pixel tiles, K = 75
+    (9, 8, 60, 60, 96, 3, 3, 1, 1, 1, 1),       # 224-pixel tiles: ragged channels and pixels
+    (96, 8, 61, 59, 64, 4, 2, 2, 3, 1, 0),      # 224-pixel tiles: strided, even kernel
 ])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_conv2d_integer_inputs_bit_exact(oracle, dev, shape, with_bias):
@@ -110,3 +113,64 @@ def test_conv2d_seam_host_buffers(oracle, dev):
                                            y.ctypes.data, N, C, H, W, OH + 1, OW, OC, kH, kW,
                                            sH, sW, pH, pW, 1)
     assert st == _lib.MJ_ERR_SHAPE
+
+
+def _conv_path(M, Ng, N):
+    """The launcher's choice (gemm_f32.hip launch_conv2d_f32): for OC >= 64
+    the 224- or 256-pixel tile kernel when its grid has >= 256 workgroups,
+    else the square tiles of the matmul engine."""
+    if M >= 64:
+        best, pick, wgs_pick = None, None, 0
+        for c in (8, 7):
+            tbn = 32 * c
+            wgs = ((M + 63) // 64) * ((Ng + tbn - 1) // tbn) * N
+            cost = (wgs + 255) // 256 * tbn
+            if best is None or cost < best:
+                best, pick, wgs_pick = cost, tbn, wgs
+        if wgs_pick >= 256:
+            return pick
+    return "square"
+
+
+_IM2COL_SHAPES = [
+    # N, C, H, W, OC, kH, kW, sH, sW, pH, pW
+    (2, 16, 14, 14, 64, 3, 3, 1, 1, 1, 1),      # square tiles
+    (3, 5, 33, 47, 70, 5, 3, 2, 1, 2, 1),       # square tiles, ragged
+    (8, 32, 40, 40, 96, 3, 3, 1, 1, 1, 1),      # square tiles, two channel tiles
+    (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1),     # 224: the bench layer
+    (9, 8, 60, 60, 96, 3, 3, 1, 1, 1, 1),       # 224, ragged channel and pixel tiles
+    (96, 8, 61, 59, 64, 4, 2, 2, 3, 1, 0),      # 224, strided, even kernel, no vertical padding
+    (8, 16, 64, 64, 256, 3, 3, 1, 1, 1, 1),     # 256
+]
+
+
+def test_im2col_shapes_reach_every_conv_path():
+    paths = set()
+    for (N, C, H, W, OC, kH, kW, sH, sW, pH, pW) in _IM2COL_SHAPES:
+        OH, OW = (H + 2 * pH - kH) // sH + 1, (W + 2 * pW - kW) // sW + 1
+        paths.add(_conv_path(OC, OH * OW, N))
+    assert paths == {"square", 224, 256}
+
+
+@pytest.mark.parametrize("shape", _IM2COL_SHAPES)
+@pytest.mark.parametrize("epi", [mj.EPI_NONE, mj.EPI_RELU])
+def test_conv2d_equals_library_matmul_on_im2col(dev, shape, epi):
+    """N(0,1) data: the convolution is, bit for bit, the library's fp32
+    matmul of the flattened weight with torch's unfold of each image (an
+    exact copy of the taps, zeros in the padding), plus the bias in one fp32
+    rounding, then the activation: both run the MFMA sums in the same k
+    order."""
+    N, C, H, W, OC, kH, kW, sH, sW, pH, pW = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn((N, C, H, W), generator=g)
+    w = torch.randn((OC, C, kH, kW), generator=g) * (2.0 / (C * kH * kW)) ** 0.5
+    b = torch.rand(OC, generator=g) / 8 - 1 / 16
+    got = _conv(dev, x.numpy(), w.numpy(), b.numpy(), (sH, sW), (pH, pW), epi)
+    cols = torch.nn.functional.unfold(x.to(dev), (kH, kW), padding=(pH, pW), stride=(sH, sW))
+    wf = mj.Tensor(w.reshape(OC, -1).contiguous().to(dev))
+    for n in range(N):
+        prod = mj.matmul(wf, mj.Tensor(cols[n].contiguous())).torch
+        want = prod + b.to(dev)[:, None]
+        if epi == mj.EPI_RELU:
+            want = torch.where(want > 0, want, torch.zeros_like(want))
+        np.testing.assert_array_equal(got[n].reshape(OC, -1), want.cpu().numpy())
