@@ -468,8 +468,8 @@ def bench_copy(steps, warmup):
 
 def bench_vendor(steps, warmup):
     """torch.matmul (hipBLASLt) on the C2 inputs and on the bf16 shapes of C4
-    and C5: the vendor library's time for the same products, for comparison
-    only (run when named)."""
+    and C5, and torch's conv2d (MIOpen) on the conv2d line's layer: the vendor
+    libraries' times for the same work, for comparison only (run when named)."""
     import torch
     out = []
     for (M, N, K, name) in ((4096, 4096, 4096, "c2"), (2048, 4096, 4096, "c4_shape_bf16"),
@@ -482,6 +482,18 @@ def bench_vendor(steps, warmup):
         tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         out.append({"name": f"vendor_hipblaslt_{name}", "metric": f"torch.matmul bf16 {M}x{N}x{K}",
                     "value": tf, "unit": "TFLOP/s", "ms_per_launch": ms})
+    # MIOpen (torch's conv2d, its fastest algorithm for the shape) on the
+    # conv2d line's layer; TFLOP/s counts the direct convolution's flops
+    torch.backends.cudnn.benchmark = True
+    N, C, H, W, OC, k = 32, 64, 56, 56, 64, 3
+    x = _rand_f32((N, C, H, W), 15)
+    w = _rand_f32((OC, C, k, k), 14, float((2.0 / (C * k * k)) ** 0.5))
+    b = (torch.rand(OC, device="cuda") - 0.5) / 8
+    ms = _time_launches(lambda i: torch.nn.functional.conv2d(x, w, b, padding=1), steps, warmup)
+    tf = 2.0 * N * OC * H * W * C * k * k / (ms * 1e-3) / 1e12
+    out.append({"name": "vendor_miopen_conv2d_f32_32x64x56x56_3x3",
+                "metric": "torch.nn.functional.conv2d fp32 (direct-convolution flops)",
+                "value": tf, "unit": "TFLOP/s", "ms_per_call": ms})
     return out
 
 
