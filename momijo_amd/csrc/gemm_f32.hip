@@ -6,9 +6,8 @@
 // float, full fp32 products) or v_mfma_f64_16x16x4f64 (T = double), a TB x TB
 // tile per 256-thread workgroup (64; 128 for problems with enough tiles, where
 // each wave then runs 4 x 4 MFMA blocks per LDS fragment read instead of
-// 2 x 2; 32 for tiny latency-bound problems, one block per wave; fp32 128 x
-// 128 tiles run eight waves of 64 x 32, two per SIMD: Linear.backward at
-// 4096 2857 -> 2694 us on MI355X against four waves of 64 x 64), K stages
+// 2 x 2; 32 for tiny latency-bound problems, one block per wave; the 128 and
+// 64 tiles run eight waves, two per SIMD, of TB/2 x TB/4), K stages
 // staged through LDS (k-major, padded; 16 deep, 64 (fp32) or 32 (fp64) on the
 // 32 x 32 tiles).  Neither the tile size nor the stage depth changes any
 // output's summation order.  Tiny fp32 products whose operands are both
@@ -366,22 +365,23 @@ static hipError_t launch_fx(int64_t M, int64_t N, int64_t K, const T *A, int64_t
   constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < batches; b0 += kMaxGridY) {
     const int64_t nb = batches - b0 < kMaxGridY ? batches - b0 : kMaxGridY;
-    if (big && sizeof(T) == sizeof(float))
+    // eight waves (two per SIMD) on the 128 x 128 and 64 x 64 tiles, four on
+    // the tiny 32 x 32 ones (measured on MI355X against four waves on the same
+    // tiles: fp32 Linear.backward 4096 2857 -> 2694 us, fp32 2048^3 220 ->
+    // 207 us, 1536^3 130 -> 119 us, fp64 4096^3 3293 -> 2657 us, fp64 2048^3
+    // 411 -> 326 us)
+    if (big)
       hipLaunchKernelGGL((gemm_fx_kernel<T, 128, kFBK, false, 8>), dim3(tiles, (unsigned)nb),
                          dim3(512), 0, stream, (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn,
                          bias, epi, accum, C, ldc, bd, b0, ConvDesc{});
-    else if (big)
-      hipLaunchKernelGGL((gemm_fx_kernel<T, 128>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
-                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0, ConvDesc{});
     else if (tiny)
-      hipLaunchKernelGGL((gemm_fx_kernel<T, 32, kTinyBK<T>>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
-                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0, ConvDesc{});
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 32, kTinyBK<T>>), dim3(tiles, (unsigned)nb),
+                         dim3(256), 0, stream, (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn,
+                         bias, epi, accum, C, ldc, bd, b0, ConvDesc{});
     else
-      hipLaunchKernelGGL((gemm_fx_kernel<T, 64>), dim3(tiles, (unsigned)nb), dim3(256), 0, stream,
-                         (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn, bias, epi, accum, C,
-                         ldc, bd, b0, ConvDesc{});
+      hipLaunchKernelGGL((gemm_fx_kernel<T, 64, kFBK, false, 8>), dim3(tiles, (unsigned)nb),
+                         dim3(512), 0, stream, (int)M, (int)N, (int)K, A, sAm, sAk, B, sBk, sBn,
+                         bias, epi, accum, C, ldc, bd, b0, ConvDesc{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
