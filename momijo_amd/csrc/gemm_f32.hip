@@ -587,11 +587,15 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, flo
   ConvDesc cv;
   cv.H = (int)H; cv.W = (int)W; cv.OW = (int)OW; cv.kH = (int)kH; cv.kW = (int)kW;
   cv.sH = (int)sH; cv.sW = (int)sW; cv.pH = (int)pH; cv.pW = (int)pW;
-  // OC >= 64 and a grid of at least 256 workgroups: conv2d_fx_kernel with
+  // OC >= 64 and a grid of at least 192 workgroups: conv2d_fx_kernel with
   // 224- or 256-pixel tiles, whichever leaves fewer pixel columns on the
   // busiest CU (workgroups of all images dealt over 256 CUs; 256 on a tie).
-  // Narrower tiles of that kernel measured slower than the square tiles
-  // below (128: 158.6 us, against 137 us for 64 x 64 on the bench layer).
+  // Against the square tiles below (eight waves), MI355X: 32 x 64 x 56^2 ->
+  // 64 (448 workgroups) 126 against 145 us, 16 x 64 x 56^2 -> 64 (224) 79.5
+  // against 87.5, but 8 x 64 x 56^2 -> 64 (112) 74.5 against 49.1 and
+  // 16 x 128 x 28^2 -> 128 (128) 139 against 90.  Narrower tiles of that
+  // kernel were slower than the square ones (128 pixels: 158.6 us on the
+  // bench layer).
   if (M >= 64 && C * H * W < ((int64_t)1 << 29) && M * K < ((int64_t)1 << 29)) {
     int nbn = 0;
     int64_t best = INT64_MAX, wgs_best = 0;
@@ -605,7 +609,7 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, flo
         wgs_best = wgs;
       }
     }
-    if (wgs_best >= 256) {
+    if (wgs_best >= 192) {
       const int64_t tiles_c = ((M + 63) / 64) * ((Ng + 32 * nbn - 1) / (32 * nbn));
       if (tiles_c > INT32_MAX) return hipErrorInvalidValue;
       for (int64_t b0 = 0; b0 < N; b0 += kMaxGridY) {
@@ -641,9 +645,13 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, flo
   const int tiles = (int)tiles64;
   for (int64_t b0 = 0; b0 < N; b0 += kMaxGridY) {
     const int64_t nb = N - b0 < kMaxGridY ? N - b0 : kMaxGridY;
+    // eight waves on the 128 and 64 tiles, as the matmul (against four:
+    // 8 x 32 x 40^2 -> 96 32.4 -> 28.5 us, 4 x 64 x 56^2 -> 64 42.4 -> 32.6,
+    // 16 x 128 x 28^2 -> 128 102 -> 90, 8 x 256 x 14^2 -> 256 144 -> 107,
+    // 32 x 3 x 224^2 -> 32 (7 x 7, stride 2) 149 -> 143 us on MI355X)
     if (big)
-      hipLaunchKernelGGL((gemm_fx_kernel<float, 128, kFBK, true>), dim3(tiles, (unsigned)nb),
-                         dim3(256), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
+      hipLaunchKernelGGL((gemm_fx_kernel<float, 128, kFBK, true, 8>), dim3(tiles, (unsigned)nb),
+                         dim3(512), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
                          (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0, cv);
     else if (tiny)
       hipLaunchKernelGGL((gemm_fx_kernel<float, 32, kTinyBK<float>, true>),
@@ -651,8 +659,8 @@ hipError_t launch_conv2d_f32(const float *x, const float *w, const float *b, flo
                          w, K, (int64_t)1, x, (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0,
                          cv);
     else
-      hipLaunchKernelGGL((gemm_fx_kernel<float, 64, kFBK, true>), dim3(tiles, (unsigned)nb),
-                         dim3(256), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
+      hipLaunchKernelGGL((gemm_fx_kernel<float, 64, kFBK, true, 8>), dim3(tiles, (unsigned)nb),
+                         dim3(512), 0, stream, (int)M, (int)Ng, (int)K, w, K, (int64_t)1, x,
                          (int64_t)0, (int64_t)1, b, epi, 0, y, Ng, bd, b0, cv);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

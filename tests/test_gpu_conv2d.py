@@ -117,7 +117,7 @@ def test_conv2d_seam_host_buffers(oracle, dev):
 
 def _conv_path(M, Ng, N):
     """The launcher's choice (gemm_f32.hip launch_conv2d_f32): for OC >= 64
-    the 224- or 256-pixel tile kernel when its grid has >= 256 workgroups,
+    the 224- or 256-pixel tile kernel when its grid has >= 192 workgroups,
     else the square tiles of the matmul engine."""
     if M >= 64:
         best, pick, wgs_pick = None, None, 0
@@ -127,7 +127,7 @@ def _conv_path(M, Ng, N):
             cost = (wgs + 255) // 256 * tbn
             if best is None or cost < best:
                 best, pick, wgs_pick = cost, tbn, wgs
-        if wgs_pick >= 256:
+        if wgs_pick >= 192:
             return pick
     return "square"
 
