@@ -22,6 +22,8 @@
 // (one SDWA convert) and multiplied with fp32 accumulation; a DPP reduction
 // finishes each dot, then scale, bias and the activation are applied in fp32
 // and the result is rounded to bf16.
+#include <atomic>
+
 #include "common.h"
 #include "launch.h"
 
@@ -273,6 +275,183 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
       if (bias) v = v + bias[n];
     }
     y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+  }
+}
+
+// Skinny-M W8A16 GEMV for 3 <= M <= 16 and K = 1024 j (j <= 4): the weights
+// stream as whole row pieces and reach the MFMA through LDS.  NWV waves split
+// K (KQ = K / NWV bytes of every row each); a workgroup owns 16 TILES weight
+// rows.  For each 16-row tile a wave copies its share of the 16 rows straight
+// into its own LDS region (buffer_load ... lds, 1 KB per instruction: 1024 /
+// KQ rows of KQ contiguous bytes), two tiles in flight, then reads the MFMA
+// fragments from there: lane (r, c) takes 16 int8 of row r at 16-byte chunk
+// 4 j + c of 64-deep block j, widened exactly to bf16, the first 8 k for one
+// v_mfma_f32_16x16x32_bf16 and the other 8 for the second, against x
+// fragments of the same k that the wave loaded once, into registers, at the
+// start.  Chunk p of row r is stored at LDS chunk p ^ (r & 7), so the 8 lanes
+// of a 128-byte read phase hit distinct banks.  No barrier in the loop: a wave
+// reads only its own region.  The NWV partial 16 x 16 tiles of a row tile are
+// added in K order through LDS (deterministic), then scale, bias and the
+// activation.
+// Measured on MI355X at 11008 x 4096 (graph replay over 8 weight copies):
+// M = 3, 8, 16 13.3, 13.7, 15.1 us against 15.3, 17.3, 19.4 for
+// gemv_w8a16_mfma_kernel (16 weight rows per workgroup, x re-read per 16 rows,
+// 64 bytes of a row per load instruction); four waves of 1-KB rows 13.5, 14.1,
+// 15.6.  The copies alone (no fragment reads, no MFMA) take 9.2 us with four
+// waves, 10.8 with eight: the widening (1.5 VALU per weight) runs while only
+// one of the two slots is in flight, and a third slot does not fit the LDS.
+__device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)lds_dst, 16, off, 0, 0, 2 /* nt */);
+}
+
+// s_waitcnt immediate: vmcnt <= n, lgkmcnt and expcnt unconstrained
+constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F70; }
+
+template <int TILES, int KB, int NWV>
+__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint16_t *__restrict__ x,
+                                                                const int8_t *__restrict__ Q,
+                                                                const float *__restrict__ scales,
+                                                                const float *__restrict__ bias,
+                                                                int epi, uint16_t *__restrict__ y,
+                                                                int M, int N, int K) {
+  constexpr int NJ = 64 / NWV;         // most 64-deep blocks per wave (K <= 4096)
+  constexpr int SLOT = 65536 / NWV;    // bytes of one tile's share at K = 4096
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  f32x4 *red = (f32x4 *)(lds8 + NWV * 2 * SLOT);  // [NWV][TILES][64]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, c = lane >> 4;
+  const int n0 = blockIdx.x * 16 * TILES;
+  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
+  constexpr int KQ = 512 * KB / NWV;  // bytes of a row per wave (K = 512 KB)
+  static_assert(KQ >= 128, "eight 16-byte chunks per row share");
+  constexpr int nj = KQ / 64;    // 64-deep blocks per wave
+  constexpr int ninst = KQ / 64; // 1-KB copies per tile (16 KQ bytes)
+  const int kq0 = wave * KQ;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
+  uint8_t *mine = lds8 + wave * 2 * SLOT;
+
+  // x fragments of this wave's quarter, once
+  uint4 xa[NJ], xb[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    xa[j] = xb[j] = make_uint4(0, 0, 0, 0);
+    if (j < nj && r < M) {
+      const uint32_t xo = (uint32_t)((r * K + kq0 + 64 * j + 16 * c) * 2);
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+      xa[j] = make_uint4(a[0], a[1], a[2], a[3]);
+      xb[j] = make_uint4(b[0], b[1], b[2], b[3]);
+    }
+  }
+  // tile t's quarter -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
+  // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7)
+  auto issue = [&](int t) {
+    uint8_t *dst = mine + (t & 1) * SLOT;
+#pragma unroll
+    for (int i = 0; i < ninst; ++i) {
+      const int e = 1024 * i + 16 * lane;
+      const int rr = e / KQ, p = (e - rr * KQ) >> 4;
+      const uint32_t off = (uint32_t)((t * 16 + rr) * K + kq0 + 16 * (p ^ (rr & 7)));
+      dma16_lds(rQ, dst + 1024 * i, off);
+    }
+  };
+  issue(0);
+  if (TILES > 1) issue(1);
+  f32x4 acc[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    // tile t landed: at most the copies of tile t + 1 still outstanding
+    if (t + 1 < TILES) __builtin_amdgcn_s_waitcnt(vmcnt_imm(ninst));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    asm volatile("" ::: "memory");
+    const uint8_t *src = mine + (t & 1) * SLOT + r * KQ;
+    // four independent accumulator chains (block parity x chunk half), added
+    // in a fixed order at the end: the MFMAs of a tile do not wait on each other
+    f32x4 ch[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ch[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 qv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (j < nj) qv[j] = *(const uint4 *)(src + 16 * ((4 * j + c) ^ (r & 7)));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j < nj) {
+        const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
+        const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
+        ch[2 * (j & 1)] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w0, __builtin_bit_cast(bf16x8, xa[j]), ch[2 * (j & 1)], 0, 0, 0);
+        ch[2 * (j & 1) + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w1, __builtin_bit_cast(bf16x8, xb[j]), ch[2 * (j & 1) + 1], 0, 0, 0);
+      }
+    }
+    acc[t] = (ch[0] + ch[1]) + (ch[2] + ch[3]);
+    if (t + 2 < TILES) {
+      // this wave's fragment reads of the slot are done before it is refilled
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+      issue(t + 2);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) red[(wave * TILES + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  if (wave >= TILES) return;
+  f32x4 sum = red[(0 * TILES + wave) * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) sum += red[(w * TILES + wave) * 64 + lane];
+  // lane: x row m = lane % 16, weight rows n0 + 16 wave + 4 (lane / 16) + q
+  const int m = r;
+  if (m >= M) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = n0 + 16 * wave + 4 * c + q;
+    if (n >= N) break;
+    float v;
+    {
+#pragma clang fp contract(off)
+      v = sum[q] * scales[n];
+      if (bias) v = v + bias[n];
+    }
+    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+  }
+}
+
+template <int TILES, int KB, int NWV>
+static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const float *scales,
+                                const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
+                                int64_t K, hipStream_t stream) {
+  constexpr size_t lds = 2 * 65536 + NWV * TILES * 64 * sizeof(f32x4);
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV>;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))), dim3(NWV * 64), lds,
+                     stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+  return hipGetLastError();
+}
+
+template <int TILES, int NWV>
+static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const float *scales,
+                                const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
+                                int64_t K, hipStream_t stream) {
+  switch (K / 512) {
+#define MJ_SK(kb) \
+  case kb: return launch_skinny_k<TILES, kb, NWV>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    MJ_SK(2) MJ_SK(4) MJ_SK(6) MJ_SK(8)
+#undef MJ_SK
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -614,6 +793,8 @@ constexpr int kGemvMfmaMinM = 3;
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream) {
+  if (M >= kGemvMfmaMinM && M <= kGemvMaxM && K % 1024 == 0 && K <= 4096)
+    return launch_skinny<3, 8>(x, Q, scales, bias, epi, y, M, N, K, stream);
   if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
     // 32-bit buffer offsets over the x rows and the 64 weight rows of a workgroup
     if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 64 * K >= ((int64_t)1 << 31))

@@ -336,10 +336,14 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    (384, 1000, 2064),    # 4-way K split, partial N tile
                                    (1000, 1300, 528),    # partial M and N tiles, one K slice
                                    (256, 256, 16384),    # 8-way K split: one K slice per XCD
-                                   # skinny-M MFMA GEMV: partial 16-row tile of
-                                   # weights, K % 64 != 0, x rows < 16
-                                   (3, 4104, 1040), (16, 1000, 4096),
-                                   (7, 37, 80),
+                                   # skinny-M MFMA GEMV (K % 1024 != 0): partial
+                                   # 16-row tile of weights, K % 64 != 0, x rows < 16
+                                   (3, 4104, 1040), (7, 37, 80),
+                                   # skinny-M GEMV through LDS (K = 1024 j <= 4096):
+                                   # every K share, partial 48-row workgroups, the
+                                   # C3 weight at 3 and 16 x rows
+                                   (16, 1000, 4096), (3, 11008, 4096), (16, 11008, 4096),
+                                   (5, 4104, 1024), (8, 1000, 2048), (11, 37, 3072),
                                    # M = 1: the persistent streaming GEMV (K a
                                    # multiple of 1024) at every rows-per-wave
                                    # (1..32) and K-chunk count (1..4), with
