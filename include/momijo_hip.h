@@ -319,9 +319,10 @@ int32_t mj_quantize_rowwise_i8(const float *W, int64_t N, int64_t K, int32_t rou
                                int8_t *Q, float *scales, void *stream);
 
 /* y[M,N] = bf16(epi((x[M,K] . Q[N,K]^T) * scales[N] + bias[N])) with x bf16,
- * fp32 accumulation.  M <= 16 runs the GEMV kernels, larger M the
- * MFMA GEMM with int8 -> bf16 conversion on the way into LDS.  bias may be
- * NULL.  Needs K % 16 == 0 and 16-byte aligned x, Q, y. */
+ * fp32 accumulation.  M <= 16 (and M <= 32 when K is a multiple of 1024 up
+ * to 4096) runs the GEMV kernels, larger M the MFMA GEMM with int8 -> bf16
+ * conversion in registers.  bias may be NULL.  Needs K % 16 == 0 and 16-byte
+ * aligned x, Q, y. */
 int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                         const float *bias, int32_t epilogue, uint16_t *y,
                         int64_t M, int64_t N, int64_t K, void *stream);

@@ -97,7 +97,7 @@ int32_t refuse_capture(hipStream_t stream) {
   if (cs != hipStreamCaptureStatusNone)
     return fail(MJ_ERR_UNSUPPORTED,
                 "this call needs the library's per-stream workspace, which is not available "
-                "under graph capture (mj_quant_linear_f32_noalloc, the GEMV (M <= 16) and "
+                "under graph capture (mj_quant_linear_f32_noalloc, the GEMVs and "
                 "the GEMMs without a K split can be captured)");
   return MJ_OK;
 }
@@ -686,7 +686,7 @@ int32_t mj_linear_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
   if (!y || !scales || (K > 0 && (!x || !Q))) return fail(MJ_ERR_ARG, "null operand");
   if (K % 16 || !aligned16(x) || !aligned16(Q))
     return fail(MJ_ERR_UNSUPPORTED, "W8A16 Linear needs K %% 16 == 0 and 16-byte aligned x, Q");
-  if (M <= mj::kGemvMaxM)
+  if (mj::gemv_w8a16_takes(M, K))
     return hip_status(mj::launch_gemv_w8a16(x, Q, scales, bias, epilogue, y, M, N, K, S(stream)),
                       "gemv_w8a16 launch");
   mj::GemmNT p;
@@ -750,7 +750,7 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   mj::GemmNT dn;
   dn.A = h; dn.lda = I; dn.B = Wd; dn.ldb = I; dn.scales = sd; dn.C = y; dn.ldc = H;
   dn.M = M; dn.N = H; dn.K = I; dn.bkind = mj::B_INT8;
-  const bool down_gemv = M <= mj::kGemvMaxM;
+  const bool down_gemv = mj::gemv_w8a16_takes(M, I);
   if (int32_t st = check_tile_offsets(gu, "gate/up")) return st;
   if (!down_gemv) {
     if (int32_t st = check_tile_offsets(dn, "down")) return st;

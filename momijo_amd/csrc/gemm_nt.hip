@@ -1948,6 +1948,22 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     }
     return pl;
   }
+  if (w4i8_ok && p.M > kGemvMaxM && p.M < 256) {
+    // batched decode and short prefill: the same kernel on 128-row tiles for
+    // M <= 128, else on 256-row tiles (rows past M load zeros), the K split
+    // as below.  Against the eight-wave tiles the cost model picks, on MI355X
+    // (11008 x 4096 weights, M x 4096 x): M = 17 28.3 -> 25.3 us, M = 128
+    // 36.5 -> 29.2, M = 192 54.7 -> 36.0, M = 255 55.8 -> 39.1
+    pl.bm = p.M <= 128 ? 128 : 256;
+    pl.bn = 128;
+    pl.wm = pl.bm;
+    pl.tile_kernel = true;
+    const int64_t tiles = ((p.M + pl.bm - 1) / pl.bm) * ((p.N + 127) / 128);
+    const int64_t nk = (p.K + kBK - 1) / kBK;
+    while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
+      pl.splits *= 2;
+    return pl;
+  }
   if (w4i8_ok && p.M >= 256) {
     // the one-wave-per-SIMD int8 kernel on 256 x 128 tiles with 1 x 4 waves of
     // 256 x 32, K split until the grid covers the 256 CUs (>= 8 stages per
@@ -2035,8 +2051,12 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     else
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.tile_kernel) {
-    if (pl.bm != 256 || pl.bn != 128 || pl.wm != 256) return hipErrorInvalidValue;
-    e = launch_w4i8<256, 128, false, 256>(p, stream);
+    if (pl.bm == 128 && pl.bn == 128 && pl.wm == 128) {
+      e = launch_w4i8<128, 128, false, 128>(p, stream);
+    } else {
+      if (pl.bm != 256 || pl.bn != 128 || pl.wm != 256) return hipErrorInvalidValue;
+      e = launch_w4i8<256, 128, false, 256>(p, stream);
+    }
   } else {
     if (pl.pf2) return hipErrorInvalidValue;
     e = pl.iglp ? launch_plain<B_INT8, true, false>(pl.bm, pl.bn, p, stream)

@@ -308,7 +308,7 @@ __device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_ds
 // s_waitcnt immediate: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F70; }
 
-template <int TILES, int KB, int NWV>
+template <int TILES, int KB, int NWV, int MB>
 __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint16_t *__restrict__ x,
                                                                 const int8_t *__restrict__ Q,
                                                                 const float *__restrict__ scales,
@@ -318,7 +318,6 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
   constexpr int NJ = 64 / NWV;         // most 64-deep blocks per wave (K <= 4096)
   constexpr int SLOT = 65536 / NWV;    // bytes of one tile's share at K = 4096
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
-  f32x4 *red = (f32x4 *)(lds8 + NWV * 2 * SLOT);  // [NWV][TILES][64]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
@@ -333,20 +332,22 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
   uint8_t *mine = lds8 + wave * 2 * SLOT;
 
-  // x fragments of this wave's quarter, once
-  uint4 xa[NJ], xb[NJ];
+  // x fragments of this wave's share, once: group g holds x rows 16 g + r
+  uint4 xa[MB][NJ], xb[MB][NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    xa[j] = xb[j] = make_uint4(0, 0, 0, 0);
-    if (j < nj && r < M) {
-      const uint32_t xo = (uint32_t)((r * K + kq0 + 64 * j + 16 * c) * 2);
-      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
-      xa[j] = make_uint4(a[0], a[1], a[2], a[3]);
-      xb[j] = make_uint4(b[0], b[1], b[2], b[3]);
+  for (int g = 0; g < MB; ++g)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      xa[g][j] = xb[g][j] = make_uint4(0, 0, 0, 0);
+      if (j < nj && 16 * g + r < M) {
+        const uint32_t xo = (uint32_t)(((16 * g + r) * K + kq0 + 64 * j + 16 * c) * 2);
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+        xa[g][j] = make_uint4(a[0], a[1], a[2], a[3]);
+        xb[g][j] = make_uint4(b[0], b[1], b[2], b[3]);
+      }
     }
-  }
-  // tile t's quarter -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
+  // tile t's share -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
   // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7)
   auto issue = [&](int t) {
     uint8_t *dst = mine + (t & 1) * SLOT;
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
   };
   issue(0);
   if (TILES > 1) issue(1);
-  f32x4 acc[TILES];
+  f32x4 acc[TILES][MB];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
     // tile t landed: at most the copies of tile t + 1 still outstanding
@@ -368,11 +369,11 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     asm volatile("" ::: "memory");
     const uint8_t *src = mine + (t & 1) * SLOT + r * KQ;
-    // four independent accumulator chains (block parity x chunk half), added
-    // in a fixed order at the end: the MFMAs of a tile do not wait on each other
-    f32x4 ch[4];
+    // two independent accumulator chains per x group (the chunk halves), added
+    // in a fixed order at the end
+    f32x4 ch[MB][2];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) ch[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = 0; g < MB; ++g) ch[g][0] = ch[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     uint4 qv[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
@@ -382,13 +383,17 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
       if (j < nj) {
         const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
         const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
-        ch[2 * (j & 1)] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w0, __builtin_bit_cast(bf16x8, xa[j]), ch[2 * (j & 1)], 0, 0, 0);
-        ch[2 * (j & 1) + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w1, __builtin_bit_cast(bf16x8, xb[j]), ch[2 * (j & 1) + 1], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < MB; ++g) {
+          ch[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              w0, __builtin_bit_cast(bf16x8, xa[g][j]), ch[g][0], 0, 0, 0);
+          ch[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              w1, __builtin_bit_cast(bf16x8, xb[g][j]), ch[g][1], 0, 0, 0);
+        }
       }
     }
-    acc[t] = (ch[0] + ch[1]) + (ch[2] + ch[3]);
+#pragma unroll
+    for (int g = 0; g < MB; ++g) acc[t][g] = ch[g][0] + ch[g][1];
     if (t + 2 < TILES) {
       // this wave's fragment reads of the slot are done before it is refilled
       __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -396,37 +401,46 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
       issue(t + 2);
     }
   }
+  // every wave is past its last fragment read (and its copies have landed):
+  // the slots become the partials [NWV][TILES][MB][64]
+  __syncthreads();
+  f32x4 *red = (f32x4 *)lds8;
 #pragma unroll
-  for (int t = 0; t < TILES; ++t) red[(wave * TILES + t) * 64 + lane] = acc[t];
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int g = 0; g < MB; ++g) red[((wave * TILES + t) * MB + g) * 64 + lane] = acc[t][g];
   __syncthreads();
   if (wave >= TILES) return;
-  f32x4 sum = red[(0 * TILES + wave) * 64 + lane];
 #pragma unroll
-  for (int w = 1; w < NWV; ++w) sum += red[(w * TILES + wave) * 64 + lane];
-  // lane: x row m = lane % 16, weight rows n0 + 16 wave + 4 (lane / 16) + q
-  const int m = r;
-  if (m >= M) return;
+  for (int g = 0; g < MB; ++g) {
+    f32x4 sum = red[((0 * TILES + wave) * MB + g) * 64 + lane];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int n = n0 + 16 * wave + 4 * c + q;
-    if (n >= N) break;
-    float v;
-    {
+    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + wave) * MB + g) * 64 + lane];
+    // lane: x row m = 16 g + lane % 16, weight rows n0 + 16 wave + 4 (lane / 16) + q
+    const int m = 16 * g + r;
+    if (m >= M) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + 16 * wave + 4 * c + q;
+      if (n >= N) break;
+      float v;
+      {
 #pragma clang fp contract(off)
-      v = sum[q] * scales[n];
-      if (bias) v = v + bias[n];
+        v = sum[q] * scales[n];
+        if (bias) v = v + bias[n];
+      }
+      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
     }
-    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
   }
 }
 
-template <int TILES, int KB, int NWV>
+template <int TILES, int KB, int NWV, int MB>
 static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const float *scales,
                                 const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                                 int64_t K, hipStream_t stream) {
-  constexpr size_t lds = 2 * 65536 + NWV * TILES * 64 * sizeof(f32x4);
-  static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV>;
+  constexpr size_t lds = 2 * 65536;
+  static_assert(NWV * TILES * MB * 64 * sizeof(f32x4) <= lds, "partials fit the slots");
+  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -442,13 +456,13 @@ static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const floa
   return hipGetLastError();
 }
 
-template <int TILES, int NWV>
+template <int TILES, int NWV, int MB>
 static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const float *scales,
                                 const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                                 int64_t K, hipStream_t stream) {
   switch (K / 512) {
 #define MJ_SK(kb) \
-  case kb: return launch_skinny_k<TILES, kb, NWV>(x, Q, scales, bias, epi, y, M, N, K, stream);
+  case kb: return launch_skinny_k<TILES, kb, NWV, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
     MJ_SK(2) MJ_SK(4) MJ_SK(6) MJ_SK(8)
 #undef MJ_SK
     default: return hipErrorInvalidValue;
@@ -793,8 +807,10 @@ constexpr int kGemvMfmaMinM = 3;
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream) {
-  if (M >= kGemvMfmaMinM && M <= kGemvMaxM && K % 1024 == 0 && K <= 4096)
-    return launch_skinny<3, 8>(x, Q, scales, bias, epi, y, M, N, K, stream);
+  if (M >= kGemvMfmaMinM && M <= 32 && K % 1024 == 0 && K <= 4096) {
+    if (M <= 16) return launch_skinny<3, 8, 1>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    return launch_skinny<3, 8, 2>(x, Q, scales, bias, epi, y, M, N, K, stream);
+  }
   if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
     // 32-bit buffer offsets over the x rows and the 64 weight rows of a workgroup
     if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 64 * K >= ((int64_t)1 << 31))

@@ -284,7 +284,7 @@ def test_c3_gemv(oracle, dev):
     assert err <= BF16_TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16, 17, 32])
 @pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16), (17, 48)])
 def test_gemv_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M * 100 + N)
@@ -344,6 +344,11 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    # C3 weight at 3 and 16 x rows
                                    (16, 1000, 4096), (3, 11008, 4096), (16, 11008, 4096),
                                    (5, 4104, 1024), (8, 1000, 2048), (11, 37, 3072),
+                                   # two x-row groups (17..32 rows)
+                                   (17, 1000, 4096), (32, 11008, 4096), (24, 37, 1024),
+                                   # 17..255 rows past the GEMV: 128- and 256-row tiles
+                                   (33, 11008, 4096), (128, 1000, 4096), (129, 300, 2048),
+                                   (255, 520, 1024),
                                    # M = 1: the persistent streaming GEMV (K a
                                    # multiple of 1024) at every rows-per-wave
                                    # (1..32) and K-chunk count (1..4), with
