@@ -66,7 +66,7 @@ def _args():
     p.add_argument("--settle", type=float, default=0.3,
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3pack,c4,c4w8a8,c5,"
+    p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3batch,c3pack,c4,c4w8a8,c5,"
                    "qlinear,bwd,conv2d,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
@@ -226,6 +226,40 @@ def bench_c3(steps, warmup):
         "cache_hot_GBs": bytes_ / (hot_ms * 1e-3) / 1e9,
         "dispatch_floor_us": floor_ms * 1e3,
     }
+
+
+def bench_c3_batch(steps, warmup):
+    """The C3 weight (11008 x 4096 int8, per-channel scales, bias) at 4, 16
+    and 32 x rows: batched decode on the skinny GEMV, HBM-bound like C3.
+    Graph replay over 8 weight copies, as the C3 line."""
+    import torch
+    import momijo_amd as mj
+    N, K = 11008, 4096
+    W = _rand_f32((N, K), 4, 0.02)
+    q0, s = mj.quantize_rowwise_int8(W)
+    del W
+    bias = (torch.rand(N, device="cuda") - 0.5) / 8
+    copies = 8
+    qs = [q0] + [q0.clone() for _ in range(copies - 1)]
+    lins = [mj.W8Linear(q, s, bias) for q in qs]
+    out = []
+    for M in (4, 16, 32):
+        x = _rand_bf16((M, K), 30 + M)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        ms = _graph_ms_per_launch(lambda i: lins[i % copies].forward(x, out=y), 64,
+                                  max(max(steps, 400) // 64, 4))
+        bytes_ = N * K + N * 4 + M * K * 2 + N * 4 + M * N * 2
+        gbs = bytes_ / (ms * 1e-3) / 1e9
+        out.append({
+            "name": f"c3batch_int8_gemv_11008x4096_m{M}",
+            "metric": f"int8 weight-only GEMV GB/s (M={M})",
+            "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+            "bytes_per_launch": bytes_,
+            "timing": "graph replay of 64 launches rotating over 8 weight copies (> MALL)",
+        })
+    return out
 
 
 def bench_c3_pack(steps, warmup):
@@ -679,7 +713,8 @@ def main():
     head = bench_c2(a.steps, a.warmup) if want("c2") else None
     print(f"# c2 done: {head and round(head['value'], 1)} TFLOP/s", file=sys.stderr, flush=True)
     secondary = []
-    for key, fn in (("c3", bench_c3), ("c3pack", bench_c3_pack), ("c4", bench_c4),
+    for key, fn in (("c3", bench_c3), ("c3batch", bench_c3_batch), ("c3pack", bench_c3_pack),
+                    ("c4", bench_c4),
                     ("c4w8a8", bench_c4_w8a8), ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
                     ("bwd", bench_backward), ("conv2d", bench_conv2d),
                     ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
