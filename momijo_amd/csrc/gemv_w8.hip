@@ -298,8 +298,10 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
 // gemv_w8a16_mfma_kernel (16 weight rows per workgroup, x re-read per 16 rows,
 // 64 bytes of a row per load instruction); four waves of 1-KB rows 13.5, 14.1,
 // 15.6.  The copies alone (no fragment reads, no MFMA) take 9.2 us with four
-// waves, 10.8 with eight: the widening (1.5 VALU per weight) runs while only
-// one of the two slots is in flight, and a third slot does not fit the LDS.
+// waves, 10.8 with eight; the rest is the widening (1.5 VALU per weight).
+// Refilling a slot as soon as its fragments are in registers (two tiles in
+// flight during the compute) measured slower, and a third slot does not fit
+// the LDS.
 __device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void *)lds_dst, 16, off, 0, 0, 2 /* nt */);
