@@ -356,7 +356,11 @@ int32_t mj_linear_w8a8(const uint16_t *x, const int8_t *Q, const float *scales,
  * elementwise product, tensor/tensor.mojo:4373):
  *   h[M,I] = bf16(silu(x Wg^T * sg) * (x Wu^T * su))   (one fused GEMM; bf16-output silu)
  *   y[M,H] = bf16((h Wd^T) * sd)
- * Wg, Wu [I,K]; Wd [H,I]; h is a caller-owned [M,I] buffer. */
+ * Wg, Wu [I,K]; Wd [H,I]; h is a caller-owned [M,I] buffer.  The gate/up
+ * runs as a GEMV at 1-4 x rows (K <= 16384) and at 5-32 rows when K = 1024 j
+ * <= 4096, the down projection as mj_linear_w8a16 runs [M,I] x [H,I]^T; with
+ * both as GEMVs the call needs no workspace and can be captured into a HIP
+ * graph. */
 int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
                      const int8_t *Wu, const float *su, const int8_t *Wd, const float *sd,
                      uint16_t *h, uint16_t *y, int64_t M, int64_t K, int64_t I, int64_t H,

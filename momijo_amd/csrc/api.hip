@@ -750,17 +750,24 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   mj::GemmNT dn;
   dn.A = h; dn.lda = I; dn.B = Wd; dn.ldb = I; dn.scales = sd; dn.C = y; dn.ldc = H;
   dn.M = M; dn.N = H; dn.K = I; dn.bkind = mj::B_INT8;
+  // decode sizes: either projection as a GEMV (no workspace)
+  const bool gu_gemv = I > 0 && mj::gemv_gateup_w8a16_takes(M, K);
   const bool down_gemv = mj::gemv_w8a16_takes(M, I);
-  if (int32_t st = check_tile_offsets(gu, "gate/up")) return st;
+  if (!gu_gemv) {
+    if (int32_t st = check_tile_offsets(gu, "gate/up")) return st;
+  }
   if (!down_gemv) {
     if (int32_t st = check_tile_offsets(dn, "down")) return st;
   }
   // both plans first: one workspace of the larger size is acquired before
   // anything is enqueued (the two GEMMs run in order on the stream, so they
   // can share it)
-  const mj::GemmPlan pgu = mj::plan_gemm_nt(gu);
-  mj::GemmPlan pdn;
-  size_t ws = pgu.workspace_bytes(gu);
+  mj::GemmPlan pgu, pdn;
+  size_t ws = 0;
+  if (!gu_gemv) {
+    pgu = mj::plan_gemm_nt(gu);
+    ws = pgu.workspace_bytes(gu);
+  }
   if (!down_gemv) {
     pdn = mj::plan_gemm_nt(dn);
     const size_t wd = pdn.workspace_bytes(dn);
@@ -770,7 +777,14 @@ int32_t mj_mlp_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg, const
   if (ws) {
     if (int32_t st = lease.acquire(ws, S(stream))) return st;
   }
-  if (int32_t st = launch_planned(gu, pgu, lease.ptr, S(stream), "gate/up")) return st;
+  if (gu_gemv) {
+    if (int32_t st = hip_status(mj::launch_gemv_gateup_w8a16(x, Wg, sg, Wu, su, h, M, I, K,
+                                                             S(stream)),
+                                "gate/up gemv launch"))
+      return st;
+  } else if (int32_t st = launch_planned(gu, pgu, lease.ptr, S(stream), "gate/up")) {
+    return st;
+  }
   if (down_gemv)
     return hip_status(mj::launch_gemv_w8a16(h, Wd, sd, nullptr, MJ_EPI_NONE, y, M, H, I,
                                             S(stream)),

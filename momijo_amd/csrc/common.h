@@ -171,6 +171,17 @@ __device__ __forceinline__ float silu_b16(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
+// acc * s + b in fp32, one rounding each (the per-column scale and bias of
+// the int8-weight epilogues)
+__device__ __forceinline__ float epi_scale_bias(float acc, float s, float b, bool has_s,
+                                                bool has_b) {
+#pragma clang fp contract(off)
+  float v = acc;
+  if (has_s) v = v * s;
+  if (has_b) v = v + b;
+  return v;
+}
+
 __device__ __forceinline__ float apply_epi_b16(int epi, float v) {
   switch (epi) {
     case EPI_GELU_TANH: return gelu_b16(v);

@@ -48,15 +48,6 @@ namespace mj {
 
 constexpr int kBK = 64;  // K per pipeline stage
 
-__device__ __forceinline__ float epi_scale_bias(float acc, float s, float b, bool has_s,
-                                                bool has_b) {
-#pragma clang fp contract(off)
-  float v = acc;
-  if (has_s) v = v * s;
-  if (has_b) v = v + b;
-  return v;
-}
-
 // int8 x16 (one 16-byte word) -> 16 bf16 (exact), as two 16-byte words.
 __device__ __forceinline__ void i8x16_to_bf16x16(const uint4 &q, uint4 &lo, uint4 &hi) {
   uint32_t w[4] = {q.x, q.y, q.z, q.w};

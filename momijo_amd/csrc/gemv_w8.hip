@@ -278,7 +278,10 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
   }
 }
 
-// Skinny-M W8A16 GEMV for 3 <= M <= 16 and K = 1024 j (j <= 4): the weights
+// Skinny-M W8A16 GEMV for 3 <= M <= 32 (MB groups of 16 x rows) and K = 1024 j
+// (j <= 4), plain or the FFN's gate/up (GATEUP: the workgroup's tiles alternate
+// 16 gate rows and the 16 up rows of the same output columns, and the epilogue
+// forms bf16(silu(g sg) (u su)) from the two fp32 tile sums): the weights
 // stream as whole row pieces and reach the MFMA through LDS.  NWV waves split
 // K (KQ = K / NWV bytes of every row each); a workgroup owns 16 TILES weight
 // rows.  For each 16-row tile a wave copies its share of the 16 rows straight
@@ -310,27 +313,29 @@ __device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_ds
 // s_waitcnt immediate: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F70; }
 
-template <int TILES, int KB, int NWV, int MB>
-__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint16_t *__restrict__ x,
-                                                                const int8_t *__restrict__ Q,
-                                                                const float *__restrict__ scales,
-                                                                const float *__restrict__ bias,
-                                                                int epi, uint16_t *__restrict__ y,
-                                                                int M, int N, int K) {
+template <int TILES, int KB, int NWV, int MB, bool GATEUP>
+__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
+    const float *__restrict__ scales, const float *__restrict__ scales2,
+    const float *__restrict__ bias, int epi, uint16_t *__restrict__ y, int M, int N, int K) {
+  constexpr int TP = GATEUP ? TILES / 2 : TILES;  // 16-column output tiles
+  static_assert(!GATEUP || TILES % 2 == 0, "gate/up tiles come in pairs");
   constexpr int NJ = 64 / NWV;         // most 64-deep blocks per wave (K <= 4096)
   constexpr int SLOT = 65536 / NWV;    // bytes of one tile's share at K = 4096
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
-  const int n0 = blockIdx.x * 16 * TILES;
-  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
+  const int n0 = blockIdx.x * 16 * TP;
+  const int rows = N - n0 < 16 * TP ? N - n0 : 16 * TP;
   constexpr int KQ = 512 * KB / NWV;  // bytes of a row per wave (K = 512 KB)
   static_assert(KQ >= 128, "eight 16-byte chunks per row share");
   constexpr int nj = KQ / 64;    // 64-deep blocks per wave
   constexpr int ninst = KQ / 64; // 1-KB copies per tile (16 KQ bytes)
   const int kq0 = wave * KQ;
   const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rQ2 =
+      make_rsrc((GATEUP ? Q2 : Q) + (size_t)n0 * K, (int64_t)rows * K);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
   uint8_t *mine = lds8 + wave * 2 * SLOT;
 
@@ -341,24 +346,29 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       xa[g][j] = xb[g][j] = make_uint4(0, 0, 0, 0);
-      if (j < nj && 16 * g + r < M) {
-        const uint32_t xo = (uint32_t)(((16 * g + r) * K + kq0 + 64 * j + 16 * c) * 2);
+      if (j < nj) {
+        const uint32_t xo = 16 * g + r < M
+                                ? (uint32_t)(((16 * g + r) * K + kq0 + 64 * j + 16 * c) * 2)
+                                : kOobOffset;
         const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+        const u32x4 b =
+            __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
         xa[g][j] = make_uint4(a[0], a[1], a[2], a[3]);
         xb[g][j] = make_uint4(b[0], b[1], b[2], b[3]);
       }
     }
   // tile t's share -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
-  // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7)
+  // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7).
+  // GATEUP: tile 2 j is gate rows 16 j.., tile 2 j + 1 the up rows of the same columns
   auto issue = [&](int t) {
     uint8_t *dst = mine + (t & 1) * SLOT;
+    const int tr = GATEUP ? t >> 1 : t;
 #pragma unroll
     for (int i = 0; i < ninst; ++i) {
       const int e = 1024 * i + 16 * lane;
       const int rr = e / KQ, p = (e - rr * KQ) >> 4;
-      const uint32_t off = (uint32_t)((t * 16 + rr) * K + kq0 + 16 * (p ^ (rr & 7)));
-      dma16_lds(rQ, dst + 1024 * i, off);
+      const uint32_t off = (uint32_t)((tr * 16 + rr) * K + kq0 + 16 * (p ^ (rr & 7)));
+      dma16_lds((GATEUP && (t & 1)) ? rQ2 : rQ, dst + 1024 * i, off);
     }
   };
   issue(0);
@@ -412,13 +422,21 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
 #pragma unroll
     for (int g = 0; g < MB; ++g) red[((wave * TILES + t) * MB + g) * 64 + lane] = acc[t][g];
   __syncthreads();
-  if (wave >= TILES) return;
+  if (wave >= TP) return;
+  // wave w: output columns n0 + 16 w.. (tile w, or gate tile 2 w and up tile 2 w + 1)
+  constexpr int TS = GATEUP ? 2 : 1;
 #pragma unroll
   for (int g = 0; g < MB; ++g) {
-    f32x4 sum = red[((0 * TILES + wave) * MB + g) * 64 + lane];
+    f32x4 sum = red[((0 * TILES + TS * wave) * MB + g) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + wave) * MB + g) * 64 + lane];
-    // lane: x row m = 16 g + lane % 16, weight rows n0 + 16 wave + 4 (lane / 16) + q
+    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + TS * wave) * MB + g) * 64 + lane];
+    f32x4 sum2 = sum;
+    if constexpr (GATEUP) {
+      sum2 = red[((0 * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) sum2 += red[((w * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
+    }
+    // lane: x row m = 16 g + lane % 16, output columns n0 + 16 wave + 4 (lane / 16) + q
     const int m = 16 * g + r;
     if (m >= M) continue;
 #pragma unroll
@@ -426,23 +444,34 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(const uint1
       const int n = n0 + 16 * wave + 4 * c + q;
       if (n >= N) break;
       float v;
-      {
+      if constexpr (GATEUP) {
+        const float gv = epi_scale_bias(sum[q], scales[n], 0.0f, true, false);
+        const float uv = epi_scale_bias(sum2[q], scales2[n], 0.0f, true, false);
+        {
 #pragma clang fp contract(off)
-        v = sum[q] * scales[n];
-        if (bias) v = v + bias[n];
+          v = silu_b16(gv) * uv;
+        }
+      } else {
+        {
+#pragma clang fp contract(off)
+          v = sum[q] * scales[n];
+          if (bias) v = v + bias[n];
+        }
+        v = apply_epi_b16(epi, v);
       }
-      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
     }
   }
 }
 
-template <int TILES, int KB, int NWV, int MB>
-static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const float *scales,
-                                const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
-                                int64_t K, hipStream_t stream) {
+template <int TILES, int KB, int NWV, int MB, bool GATEUP>
+static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                  const float *scales, const float *scales2, const float *bias,
+                                  int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                                  hipStream_t stream) {
   constexpr size_t lds = 2 * 65536;
   static_assert(NWV * TILES * MB * 64 * sizeof(f32x4) <= lds, "partials fit the slots");
-  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB>;
+  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB, GATEUP>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -453,20 +482,213 @@ static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const floa
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))), dim3(NWV * 64), lds,
-                     stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+  constexpr int cols = 16 * (GATEUP ? TILES / 2 : TILES);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + cols - 1) / cols)), dim3(NWV * 64), lds, stream,
+                     x, Q, Q2, scales, scales2, bias, epi, y, (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
 
-template <int TILES, int NWV, int MB>
-static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const float *scales,
-                                const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
-                                int64_t K, hipStream_t stream) {
+template <int TILES, int NWV, int MB, bool GATEUP = false>
+static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                const float *scales, const float *scales2, const float *bias,
+                                int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                                hipStream_t stream) {
   switch (K / 512) {
-#define MJ_SK(kb) \
-  case kb: return launch_skinny_k<TILES, kb, NWV, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
+#define MJ_SK(kb)                                                                             \
+  case kb:                                                                                    \
+    return launch_skinny_k<TILES, kb, NWV, MB, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, \
+                                                       M, N, K, stream);
     MJ_SK(2) MJ_SK(4) MJ_SK(6) MJ_SK(8)
 #undef MJ_SK
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// The skinny GEMV at K > 4096 (the FFN's down projection at K = 11008), up to
+// 16 x rows.  K is taken in NP passes: NP - 1 of 4096 bytes of every row and a
+// last one of 512 KBL bytes that covers the rest (K rounded up to 1024).  A
+// step is one (pass, tile) pair, passes outermost: each wave copies its
+// 4096 / NWV-byte (last pass 64 KBL) share of the tile's 16 rows into its own
+// LDS slot exactly as the K <= 4096 kernel does (two steps in flight), and
+// multiplies it against the x fragments of that pass, which sit in one of two
+// register sets: the next pass's x loads are issued just before its first
+// copy, so the wait for that copy also covers them, while the current pass
+// still reads the other set.  Where a pass runs past K the x fragments are
+// zero (their loads are out of range) and the weight bytes there (the next
+// row's first bytes, or zero past the buffer) add exact zeros.  The tile
+// sums build up over the passes in registers; the waves' partials are added
+// in K order through LDS at the end, as above.
+template <int NP, int KBL, int TILES, int NWV>
+__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_long_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q,
+    const float *__restrict__ scales, const float *__restrict__ bias, int epi,
+    uint16_t *__restrict__ y, int M, int N, int K) {
+  constexpr int SLOT = 65536 / NWV;  // a full pass's share of one tile
+  constexpr int KQF = 4096 / NWV;    // bytes of a row per wave, full pass
+  constexpr int KQL = 512 * KBL / NWV;
+  static_assert(KQL >= 128 && KQL <= KQF, "eight 16-byte chunks per row share");
+  constexpr int NJ = KQF / 64;
+  constexpr int STEPS = NP * TILES;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, c = lane >> 4;
+  const int n0 = blockIdx.x * 16 * TILES;
+  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
+  uint8_t *mine = lds8 + wave * 2 * SLOT;
+
+  uint4 xa[2][NJ], xb[2][NJ];
+  // x fragments of pass p into set p & 1: lane (r, c) block j holds x row r,
+  // k = 4096 p + KQ wave + 64 j + 16 c .. + 15 (zero at k >= K or r >= M;
+  // K % 16 == 0 keeps a fragment all in or all out)
+  auto load_x = [&](int p) {
+    const int KQ = p + 1 < NP ? KQF : KQL;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j < KQ / 64) {
+        const int k = 4096 * p + wave * KQ + 64 * j + 16 * c;
+        const uint32_t xo = r < M && k < K ? (uint32_t)((r * K + k) * 2) : kOobOffset;
+        const uint32_t xo2 = xo == kOobOffset ? xo : xo + 16;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo2, 0, 0);
+        xa[p & 1][j] = make_uint4(a[0], a[1], a[2], a[3]);
+        xb[p & 1][j] = make_uint4(b[0], b[1], b[2], b[3]);
+      }
+    }
+  };
+  // vector memory instructions of one step's copies and of one pass's x loads
+  constexpr int kCopiesF = KQF / 64, kCopiesL = KQL / 64;
+  constexpr int kXLoadsF = 2 * kCopiesF, kXLoadsL = 2 * kCopiesL;
+  // step st = (pass p, tile t) -> slot st & 1, as the K <= 4096 kernel's copies
+  auto issue = [&](int st) {
+    const int p = st / TILES, t = st % TILES;
+    const int KQ = p + 1 < NP ? KQF : KQL;
+    uint8_t *dst = mine + (st & 1) * SLOT;
+#pragma unroll
+    for (int i = 0; i < KQF / 64; ++i) {
+      if (i < KQ / 64) {
+        const int e = 1024 * i + 16 * lane;
+        const int rr = e / KQ, ch = (e - rr * KQ) >> 4;
+        const uint32_t off =
+            (uint32_t)((t * 16 + rr) * K + 4096 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
+        dma16_lds(rQ, dst + 1024 * i, off);
+      }
+    }
+  };
+  load_x(0);
+  issue(0);
+  if (STEPS > 1) {
+    if (TILES == 1) load_x(1);
+    issue(1);
+  }
+  f32x4 acc[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int p = st / TILES, t = st % TILES;
+    const int KQ = p + 1 < NP ? KQF : KQL;
+    // step st landed (and its pass's x): at most step st + 1's copies, and the
+    // x loads of the pass it opens, still outstanding
+    if (st + 1 < STEPS) {
+      const bool opens = (st + 1) % TILES == 0, last = (st + 1) / TILES + 1 == NP;
+      if (opens && last) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesL + kXLoadsL));
+      else if (opens) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesF + kXLoadsF));
+      else if (last) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesL));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesF));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    asm volatile("" ::: "memory");
+    const uint8_t *src = mine + (st & 1) * SLOT + r * KQ;
+    f32x4 ch0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, ch1 = ch0;
+    uint4 qv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (j < KQ / 64) qv[j] = *(const uint4 *)(src + 16 * ((4 * j + c) ^ (r & 7)));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j < KQ / 64) {
+        const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
+        const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
+        ch0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w0, __builtin_bit_cast(bf16x8, xa[p & 1][j]), ch0, 0, 0, 0);
+        ch1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w1, __builtin_bit_cast(bf16x8, xb[p & 1][j]), ch1, 0, 0, 0);
+      }
+    }
+    acc[t] += ch0 + ch1;
+    if (st + 2 < STEPS) {
+      // this wave's fragment reads of the slot are done before it is refilled
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+      if ((st + 2) % TILES == 0) load_x((st + 2) / TILES);
+      issue(st + 2);
+    }
+  }
+  __syncthreads();
+  f32x4 *red = (f32x4 *)lds8;
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) red[(wave * TILES + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  if (wave >= TILES) return;
+  f32x4 sum = red[wave * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) sum += red[(w * TILES + wave) * 64 + lane];
+  if (r >= M) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = n0 + 16 * wave + 4 * c + q;
+    if (n >= N) break;
+    float v;
+    {
+#pragma clang fp contract(off)
+      v = sum[q] * scales[n];
+      if (bias) v = v + bias[n];
+    }
+    y[(size_t)r * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+  }
+}
+
+template <int NP, int KBL, int TILES>
+static hipError_t launch_skinny_long_k(const uint16_t *x, const int8_t *Q, const float *scales,
+                                       const float *bias, int epi, uint16_t *y, int64_t M,
+                                       int64_t N, int64_t K, hipStream_t stream) {
+  constexpr int NWV = 8;
+  constexpr size_t lds = 2 * 65536;
+  auto kern = gemv_w8a16_skinny_long_kernel<NP, KBL, TILES, NWV>;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))),
+                     dim3(NWV * 64), lds, stream, x, Q, scales, bias, epi, y, (int)M, (int)N,
+                     (int)K);
+  return hipGetLastError();
+}
+
+// K = 4096 (NP - 1) + 512 KBL after rounding K up to 1024 (4096 < K <= 16384)
+template <int TILES>
+static hipError_t launch_skinny_long(const uint16_t *x, const int8_t *Q, const float *scales,
+                                     const float *bias, int epi, uint16_t *y, int64_t M,
+                                     int64_t N, int64_t K, hipStream_t stream) {
+  const int64_t kp = (K + 1023) / 1024;  // 1-KB units
+  const int np = (int)((kp + 3) / 4), kbl = (int)(2 * (kp - 4 * (np - 1)));
+  switch (np * 10 + kbl) {
+#define MJ_SL(np_, kbl_)                                                                      \
+  case np_ * 10 + kbl_:                                                                       \
+    return launch_skinny_long_k<np_, kbl_, TILES>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    MJ_SL(2, 2) MJ_SL(2, 4) MJ_SL(2, 6) MJ_SL(2, 8) MJ_SL(3, 2) MJ_SL(3, 4) MJ_SL(3, 6)
+    MJ_SL(3, 8) MJ_SL(4, 2) MJ_SL(4, 4) MJ_SL(4, 6) MJ_SL(4, 8)
+#undef MJ_SL
     default: return hipErrorInvalidValue;
   }
 }
@@ -724,6 +946,375 @@ __global__ __launch_bounds__(256) void gemv_w8a16_ksplit_kernel(
   }
 }
 
+// The K-split GEMV for one x row at other K (K % 16 == 0, K <= 4096 CPL) and
+// the FFN's fused gate/up at one x row.  As gemv_w8a16_ksplit_kernel: the 4
+// waves split K, lane l of wave w taking 16-byte chunks 64 w + l + 256 c (c <
+// CPL) of every row, D rows in flight per wave, four rows' lane sums reduced
+// together, the waves' partials added in wave order.  GATEUP: the workgroup's
+// rows alternate gate row n and up row n of output column n (weights Q and
+// Q2, scales and scales2), and column n gets bf16(silu(g sg[n]) * (u su[n]))
+// from the fp32 sums, as the GEMM's gate/up epilogue.
+template <int RW, int D, int CPL, bool GATEUP>
+__global__ __launch_bounds__(256) void gemv_w8a16_ksplit_g_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
+    const float *__restrict__ scales, const float *__restrict__ scales2,
+    const float *__restrict__ bias, int epi, uint16_t *__restrict__ y, int N, int K) {
+  constexpr int NG = (RW + 3) / 4;  // groups of four rows reduced together
+  constexpr int NS = D + 1;         // weight register slots
+  constexpr int COLS = GATEUP ? RW / 2 : RW;
+  static_assert(!GATEUP || RW % 2 == 0, "gate/up rows come in pairs");
+  static_assert(COLS <= 64, "one output per lane of wave 0");
+  __shared__ float part[4][NG * 4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col0 = blockIdx.x * COLS;
+  const int cols = N - col0 < COLS ? N - col0 : COLS;
+  const int rows = GATEUP ? 2 * cols : cols;
+  const int nch = K / 16;
+  const int ch0 = wave * 64 + lane;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)col0 * K, (int64_t)cols * K);
+  const __amdgpu_buffer_rsrc_t rQ2 =
+      make_rsrc((GATEUP ? Q2 : Q) + (size_t)col0 * K, (int64_t)cols * K);
+  uint4 q[NS][CPL];
+  auto issue = [&](int r, int slot) {
+    const int rr = GATEUP ? r >> 1 : r;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = ch0 + 256 * c;
+      const uint32_t off = r < rows && ch < nch ? (uint32_t)(rr * K + ch * 16) : kOobOffset;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (r & 1)) ? rQ2 : rQ, off,
+                                                            0, 2 /* nt */);
+      q[slot][c] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  issue(0, 0);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)K * 2);
+  u32x4 xa[CPL], xb[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = ch0 + 256 * c;
+    const uint32_t xo = ch < nch ? (uint32_t)(ch * 32) : kOobOffset;
+    xa[c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+    xb[c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
+  }
+#pragma unroll
+  for (int d = 1; d < D; ++d) issue(d, d);
+  // wave 0's scales (and bias) of its outputs
+  float my_s = 1.0f, my_s2 = 1.0f, my_b = 0.0f;
+  if (wave == 0) {
+    const int t = lane < cols ? lane : cols - 1;
+    my_s = scales[col0 + t];
+    if (GATEUP) my_s2 = scales2[col0 + t];
+    else my_b = (bias ? bias : scales)[col0 + t];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float xf[CPL][16];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const uint32_t xw[8] = {xa[c][0], xa[c][1], xa[c][2], xa[c][3],
+                            xb[c][0], xb[c][1], xb[c][2], xb[c][3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xf[c][2 * e] = __uint_as_float(xw[e] << 16);
+      xf[c][2 * e + 1] = __uint_as_float(xw[e] & 0xFFFF0000u);
+    }
+  }
+  float p4[4];
+#pragma unroll
+  for (int r = 0; r < NG * 4; ++r) {
+    float a = 0.0f;
+    if (r < RW) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (r + D < RW) issue(r + D, (r + D) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint32_t qw[4] = {q[r % NS][c].x, q[r % NS][c].y, q[r % NS][c].z, q[r % NS][c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t v = (int32_t)qw[e];
+          a += xf[c][4 * e + 0] * (float)((v << 24) >> 24);
+          a += xf[c][4 * e + 1] * (float)((v << 16) >> 24);
+          a += xf[c][4 * e + 2] * (float)((v << 8) >> 24);
+          a += xf[c][4 * e + 3] * (float)(v >> 24);
+        }
+      }
+    }
+    p4[r % 4] = a;
+    if (r % 4 == 3) {
+      // every lane of 16-lane row j holds the wave's partial of row r - 3 + j;
+      // one lane of each row stores it (no partial stays live across the loop)
+      const float t = reduce4_rows(p4[0], p4[1], p4[2], p4[3]);
+      if ((lane & 15) == ((r / 4) & 15)) part[wave][r - 3 + (lane >> 4)] = t;
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || lane >= cols) return;
+  const int n = col0 + lane;
+  if (GATEUP) {
+    const int rg = 2 * lane, ru = 2 * lane + 1;
+    const float g = ((part[0][rg] + part[1][rg]) + part[2][rg]) + part[3][rg];
+    const float u = ((part[0][ru] + part[1][ru]) + part[2][ru]) + part[3][ru];
+    float h;
+    {
+#pragma clang fp contract(off)
+      const float gv = epi_scale_bias(g, my_s, 0.0f, true, false);
+      const float uv = epi_scale_bias(u, my_s2, 0.0f, true, false);
+      h = silu_b16(gv) * uv;
+    }
+    y[n] = (uint16_t)f32_to_bf16_bits(h);
+  } else {
+    float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    {
+#pragma clang fp contract(off)
+      v = v * my_s;
+      if (bias) v = v + my_b;
+    }
+    y[n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+  }
+}
+
+template <int RW, int CPL, bool GATEUP>
+static hipError_t launch_ksplit_g(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                  const float *scales, const float *scales2, const float *bias,
+                                  int epi, uint16_t *y, int64_t N, int64_t K,
+                                  hipStream_t stream) {
+  // rows in flight per wave: 8 one-chunk rows, 4 rows of 3 or 4 chunks (the
+  // same bytes in flight within registers)
+  constexpr int DM = CPL >= 3 ? 4 : 8;
+  constexpr int D = RW < DM ? RW : DM;
+  constexpr int COLS = GATEUP ? RW / 2 : RW;
+  const unsigned grid = (unsigned)((N + COLS - 1) / COLS);
+  hipLaunchKernelGGL((gemv_w8a16_ksplit_g_kernel<RW, D, CPL, GATEUP>), dim3(grid), dim3(256), 0,
+                     stream, x, Q, Q2, scales, scales2, bias, epi, y, (int)N, (int)K);
+  return hipGetLastError();
+}
+
+// Rows per workgroup: of 4, 8, 16, 32, 48, 64 and (gate/up) 88, at most 88
+// one-chunk rows, 64 of two chunks, 48 of three, 32 of four (beyond those the
+// compiler stops unrolling the row loop and the weight slots go to scratch),
+// the one with the least ceil(workgroups / 256) * (rows + 2): the rounds of
+// workgroups over the 256 CUs times a round's rows and a fixed cost of about
+// two rows (the workgroup's x reads, its start and its reduction); ties to
+// more rows.  MI355X, one x row: 4096 x 11008 (three chunks) at 8 / 16 / 24 /
+// 32 rows 9.3 / 8.8 / 9.9 / 11.0 us; gate/up 2 x 11008 x 4096 at 88 / 64 /
+// 48 / 32 rows (250 / 344 / 459 / 688 workgroups): the FFN 25.7 / 28.6 /
+// 26.1 / 26.9 us.
+template <int CPL, bool GATEUP>
+static hipError_t launch_ksplit_g_rw(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                     const float *scales, const float *scales2,
+                                     const float *bias, int epi, uint16_t *y, int64_t N, int64_t K,
+                                     hipStream_t stream) {
+  constexpr int kRows[] = {4, 8, 16, 32, 48, 64, 88};
+  constexpr int kMaxRows = CPL >= 4 ? 32 : CPL == 3 ? 48 : CPL == 2 ? 64 : GATEUP ? 88 : 64;
+  int rw = 4;
+  int64_t best = INT64_MAX;
+  for (const int r : kRows) {
+    if (r > kMaxRows) break;
+    const int64_t wgs = (N + (GATEUP ? r / 2 : r) - 1) / (GATEUP ? r / 2 : r);
+    const int64_t cost = (wgs + 255) / 256 * (r + 2);
+    if (cost <= best) best = cost, rw = r;
+  }
+#define MJ_KG(r)                                                                        \
+  case r:                                                                               \
+    if constexpr (r <= kMaxRows)                                                        \
+      return launch_ksplit_g<r, CPL, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, N, K, \
+                                             stream);                                   \
+    break;
+  switch (rw) {
+    MJ_KG(4) MJ_KG(8) MJ_KG(16) MJ_KG(32) MJ_KG(48) MJ_KG(64) MJ_KG(88)
+  }
+#undef MJ_KG
+  return hipErrorInvalidValue;
+}
+
+// The K-split GEMV at 2..MR x rows (MR = 2 or 4, K % 16 == 0, K <= 4096 CPL),
+// plain or gate/up as gemv_w8a16_ksplit_g_kernel: the same weight stream (lane
+// l of wave w takes 16-byte chunks 64 w + l + 256 c of every row, D rows in
+// flight), but each weight chunk is widened once to eight bf16 pairs (exact)
+// and multiplied against every x row's chunk with v_dot2_f32_bf16 (two exact
+// products and the running sum per instruction), x kept as the raw bf16 pairs
+// in registers (rows past M load zeros).  Per x row the lane sums go through
+// the same four-row reduction into LDS, and the waves' partials are added in
+// wave order; thread t of the workgroup then stores x row t / cols.
+template <int RW, int D, int CPL, int MR, bool GATEUP>
+__global__ __launch_bounds__(256) void gemv_w8a16_ksplit_m_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
+    const float *__restrict__ scales, const float *__restrict__ scales2,
+    const float *__restrict__ bias, int epi, uint16_t *__restrict__ y, int M, int N, int K) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+  constexpr int NG = (RW + 3) / 4;
+  constexpr int NS = D + 1;
+  constexpr int COLS = GATEUP ? RW / 2 : RW;
+  static_assert(!GATEUP || RW % 2 == 0, "gate/up rows come in pairs");
+  static_assert(MR * COLS <= 256, "one output per thread");
+  __shared__ float part[4][MR][NG * 4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col0 = blockIdx.x * COLS;
+  const int cols = N - col0 < COLS ? N - col0 : COLS;
+  const int rows = GATEUP ? 2 * cols : cols;
+  const int nch = K / 16;
+  const int ch0 = wave * 64 + lane;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)col0 * K, (int64_t)cols * K);
+  const __amdgpu_buffer_rsrc_t rQ2 =
+      make_rsrc((GATEUP ? Q2 : Q) + (size_t)col0 * K, (int64_t)cols * K);
+  uint4 q[NS][CPL];
+  auto issue = [&](int r, int slot) {
+    const int rr = GATEUP ? r >> 1 : r;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = ch0 + 256 * c;
+      const uint32_t off = r < rows && ch < nch ? (uint32_t)(rr * K + ch * 16) : kOobOffset;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (r & 1)) ? rQ2 : rQ, off,
+                                                            0, 2 /* nt */);
+      q[slot][c] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  issue(0, 0);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
+  u32x4 xa[MR][CPL], xb[MR][CPL];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = ch0 + 256 * c;
+      const uint32_t xo = m < M && ch < nch ? (uint32_t)((m * K + ch * 16) * 2) : kOobOffset;
+      xa[m][c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+      xb[m][c] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
+    }
+#pragma unroll
+  for (int d = 1; d < D; ++d) issue(d, d);
+  __builtin_amdgcn_sched_barrier(0);
+  float p4[MR][4];
+#pragma unroll
+  for (int r = 0; r < NG * 4; ++r) {
+    float a[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) a[m] = 0.0f;
+    if (r < RW) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (r + D < RW) issue(r + D, (r + D) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const uint4 qc = q[r % NS][c];
+        const bf16x8 wl = i8x8_bf16(qc.x, qc.y), wh = i8x8_bf16(qc.z, qc.w);
+        const uint4 w0 = __builtin_bit_cast(uint4, wl), w1 = __builtin_bit_cast(uint4, wh);
+        const uint32_t wp[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const uint32_t xp[8] = {xa[m][c][0], xa[m][c][1], xa[m][c][2], xa[m][c][3],
+                                  xb[m][c][0], xb[m][c][1], xb[m][c][2], xb[m][c][3]};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            a[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wp[e]),
+                                                   __builtin_bit_cast(bf16x2, xp[e]), a[m],
+                                                   false);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) p4[m][r % 4] = a[m];
+    if (r % 4 == 3) {
+      // every lane of 16-lane row j holds x row m's partial of weight row r - 3 + j
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float t = reduce4_rows(p4[m][0], p4[m][1], p4[m][2], p4[m][3]);
+        if ((lane & 15) == ((r / 4) & 15)) part[wave][m][r - 3 + (lane >> 4)] = t;
+      }
+    }
+  }
+  __syncthreads();
+  const int m = threadIdx.x / COLS, col = threadIdx.x - m * COLS;
+  if (m >= MR || m >= M || col >= cols) return;
+  const int n = col0 + col;
+  if (GATEUP) {
+    const int rg = 2 * col, ru = 2 * col + 1;
+    const float g = ((part[0][m][rg] + part[1][m][rg]) + part[2][m][rg]) + part[3][m][rg];
+    const float u = ((part[0][m][ru] + part[1][m][ru]) + part[2][m][ru]) + part[3][m][ru];
+    float h;
+    {
+#pragma clang fp contract(off)
+      const float gv = epi_scale_bias(g, scales[n], 0.0f, true, false);
+      const float uv = epi_scale_bias(u, scales2[n], 0.0f, true, false);
+      h = silu_b16(gv) * uv;
+    }
+    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(h);
+  } else {
+    float v = ((part[0][m][col] + part[1][m][col]) + part[2][m][col]) + part[3][m][col];
+    {
+#pragma clang fp contract(off)
+      v = v * scales[n];
+      if (bias) v = v + bias[n];
+    }
+    y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+  }
+}
+
+template <int RW, int CPL, int MR, bool GATEUP>
+static hipError_t launch_ksplit_m(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                  const float *scales, const float *scales2, const float *bias,
+                                  int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                                  hipStream_t stream) {
+  constexpr int DM = CPL >= 3 ? 4 : 8;
+  constexpr int D = RW < DM ? RW : DM;
+  constexpr int COLS = GATEUP ? RW / 2 : RW;
+  const unsigned grid = (unsigned)((N + COLS - 1) / COLS);
+  hipLaunchKernelGGL((gemv_w8a16_ksplit_m_kernel<RW, D, CPL, MR, GATEUP>), dim3(grid), dim3(256),
+                     0, stream, x, Q, Q2, scales, scales2, bias, epi, y, (int)M, (int)N, (int)K);
+  return hipGetLastError();
+}
+
+// rows per workgroup by the rule of launch_ksplit_g_rw, at most 64 (two x
+// rows) or 48 (four) one-chunk rows, 16 rows of four chunks at four x rows,
+// else 32 (past those the row loop is not unrolled and spills)
+template <int CPL, int MR, bool GATEUP>
+static hipError_t launch_ksplit_m_rw(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                     const float *scales, const float *scales2,
+                                     const float *bias, int epi, uint16_t *y, int64_t M,
+                                     int64_t N, int64_t K, hipStream_t stream) {
+  constexpr int kRows[] = {4, 8, 16, 32, 48, 64, 88};
+  constexpr int kMaxRows = CPL == 1 ? (MR <= 2 ? 64 : 48) : CPL >= 4 && MR >= 4 ? 16 : 32;
+  int rw = 4;
+  int64_t best = INT64_MAX;
+  for (const int r : kRows) {
+    if (r > kMaxRows) break;
+    const int64_t wgs = (N + (GATEUP ? r / 2 : r) - 1) / (GATEUP ? r / 2 : r);
+    const int64_t cost = (wgs + 255) / 256 * (r + 2);
+    if (cost <= best) best = cost, rw = r;
+  }
+#define MJ_KM(r)                                                                          \
+  case r:                                                                                 \
+    if constexpr (r <= kMaxRows)                                                          \
+      return launch_ksplit_m<r, CPL, MR, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, \
+                                                 N, K, stream);                           \
+    break;
+  switch (rw) {
+    MJ_KM(4) MJ_KM(8) MJ_KM(16) MJ_KM(32) MJ_KM(48) MJ_KM(64) MJ_KM(88)
+  }
+#undef MJ_KM
+  return hipErrorInvalidValue;
+}
+
+template <int MR, bool GATEUP>
+static hipError_t launch_ksplit_m_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                                    const float *scales, const float *scales2, const float *bias,
+                                    int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                                    hipStream_t stream) {
+  if (K <= 4096)
+    return launch_ksplit_m_rw<1, MR, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, K,
+                                             stream);
+  if (K <= 8192)
+    return launch_ksplit_m_rw<2, MR, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, K,
+                                             stream);
+  if (K <= 12288)
+    return launch_ksplit_m_rw<3, MR, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, K,
+                                             stream);
+  return launch_ksplit_m_rw<4, MR, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, K,
+                                           stream);
+}
+
 // Rows per workgroup of the K-split GEMV: the fewest of these that keep the
 // grid within kGemvStreamMaxWgs workgroups (N <= 252 * 64 rows).
 template <int RW>
@@ -809,10 +1400,25 @@ constexpr int kGemvMfmaMinM = 3;
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream) {
+  if (M == 2 && K <= 16384)
+    // 11008 x 4096: 10.1-10.3 us against 11.6-12.3 on the two-rows-per-wave
+    // kernel; 4096 x 11008: 10.1 against 14.4 on the long-K MFMA GEMV
+    return launch_ksplit_m_k<2, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K,
+                                       stream);
   if (M >= kGemvMfmaMinM && M <= 32 && K % 1024 == 0 && K <= 4096) {
-    if (M <= 16) return launch_skinny<3, 8, 1>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    return launch_skinny<3, 8, 2>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    if (M <= 16)
+      return launch_skinny<3, 8, 1>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
+    return launch_skinny<3, 8, 2>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
   }
+  if (M >= 3 && M <= 4 && K <= 16384)
+    // 4096 x 11008: 12.6 us against 14.7 on the long-K MFMA GEMV below
+    return launch_ksplit_m_k<4, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K,
+                                       stream);
+  if (M >= 5 && M <= kGemvMaxM && K > 4096 && K <= 16384)
+    // one 16-row tile per workgroup: 4096 x 11008 at 1 / 2 / 3 tiles (256 / 128
+    // / 86 workgroups) measured 0 / 2.8 / 6.6 us apart over the decode FFN at
+    // M = 16
+    return launch_skinny_long<1>(x, Q, scales, bias, epi, y, M, N, K, stream);
   if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
     // 32-bit buffer offsets over the x rows and the 64 weight rows of a workgroup
     if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 64 * K >= ((int64_t)1 << 31))
@@ -838,9 +1444,47 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
     else launch_stream_rw<4>(x, Q, scales, bias, epi, y, N, K, stream);
     return hipGetLastError();
   }
+  if (M == 1 && K > 4096 && K <= 16384) {
+    if (K <= 8192)
+      return launch_ksplit_g_rw<2, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, N, K,
+                                          stream);
+    if (K <= 12288)
+      return launch_ksplit_g_rw<3, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, N, K,
+                                          stream);
+    return launch_ksplit_g_rw<4, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, N, K,
+                                        stream);
+  }
   if (M <= 1) return launch_mb<1>(x, Q, scales, bias, epi, y, M, N, K, stream);
   if (M <= 2) return launch_mb<2>(x, Q, scales, bias, epi, y, M, N, K, stream);
   return hipErrorInvalidValue;  // M > kGemvMaxM is the GEMM's
+}
+
+// The FFN's gate/up at M x rows (gemv_gateup_w8a16_takes): h[m][n] =
+// bf16(silu(x[m] . Wg[n] * sg[n]) * (x[m] . Wu[n] * su[n])), 16-byte aligned
+// x, Wg, Wu.
+hipError_t launch_gemv_gateup_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
+                                    const int8_t *Wu, const float *su, uint16_t *h, int64_t M,
+                                    int64_t N, int64_t K, hipStream_t stream) {
+  if (!gemv_gateup_w8a16_takes(M, K)) return hipErrorInvalidValue;
+  if (M == 2)  // 2 x 11008 x 4096: 17.3 us against 20.3 on the skinny MFMA GEMV
+    return launch_ksplit_m_k<2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+  if (M <= 4 && (K % 1024 || K > 4096))  // (K = 1024 j <= 4096: 21.5 us here, 20.3 there)
+    return launch_ksplit_m_k<4, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+  if (M >= 2) {
+    // three gate/up tile pairs (48 columns) per workgroup: the decode FFN
+    // (2 x 11008 x 4096 gate/up) at M = 4 measured 51.3 / 50.1 / 45.0 / 45.1 us
+    // with 1 / 2 / 3 / 4 pairs (688 / 344 / 230 / 172 workgroups)
+    if (M <= 16)
+      return launch_skinny<6, 8, 1, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+    return launch_skinny<6, 8, 2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+  }
+  if (K <= 4096)
+    return launch_ksplit_g_rw<1, true>(x, Wg, Wu, sg, su, nullptr, 0, h, N, K, stream);
+  if (K <= 8192)
+    return launch_ksplit_g_rw<2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, N, K, stream);
+  if (K <= 12288)
+    return launch_ksplit_g_rw<3, true>(x, Wg, Wu, sg, su, nullptr, 0, h, N, K, stream);
+  return launch_ksplit_g_rw<4, true>(x, Wg, Wu, sg, su, nullptr, 0, h, N, K, stream);
 }
 
 }  // namespace mj

@@ -115,6 +115,19 @@ inline bool gemv_w8a16_takes(int64_t M, int64_t K) {
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
                              int64_t K, hipStream_t stream);
+// Whether launch_gemv_gateup_w8a16 takes the FFN's gate/up at M x rows: 1..4
+// rows at K % 16 == 0, K <= 16384 (the K-split GEMVs), 5..32 rows at K = 1024 j
+// <= 4096 (the skinny MFMA GEMV).
+inline bool gemv_gateup_w8a16_takes(int64_t M, int64_t K) {
+  if (K <= 0 || K % 16 || M < 1) return false;
+  if (M <= 4) return K <= 16384;
+  return M <= 32 && K % 1024 == 0 && K <= 4096;
+}
+// The FFN's gate/up as a GEMV: h [M,N] = bf16(silu(x Wg^T * sg) * (x Wu^T *
+// su)) for the shapes gemv_gateup_w8a16_takes accepts; 16-byte aligned x, Wg, Wu.
+hipError_t launch_gemv_gateup_w8a16(const uint16_t *x, const int8_t *Wg, const float *sg,
+                                    const int8_t *Wu, const float *su, uint16_t *h, int64_t M,
+                                    int64_t N, int64_t K, hipStream_t stream);
 
 // ---- quant.hip -------------------------------------------------------------
 hipError_t launch_quantize_rowwise(const float *W, int64_t N, int64_t K, int rounding,

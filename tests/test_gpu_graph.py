@@ -238,3 +238,47 @@ def test_graph_replays_match_eager(oracle, dev):
         for name, g_, w_ in zip(names, got, want):
             np.testing.assert_array_equal(g_, w_, err_msg=f"replay {rep}: {name}")
         assert np.any(got[0] != 0) and np.all(np.isfinite(got[2]))
+
+
+def test_decode_ffn_graph_replays_match_eager(oracle, dev):
+    """The FFN at one x row needs no workspace (gate/up GEMV, then the down
+    GEMV at K = 11008): it captures, and three replays over fresh inputs, with
+    eager calls and synchronizations between them, equal the eager result bit
+    for bit."""
+    K, I, H = 4096, 11008, 4096
+    mk = lambda n, k, seed: mj.W8Linear(*mj.quantize_rowwise_int8(  # noqa: E731
+        to_dev(oracle.randn_f32((n, k), std=0.02, seed=seed), dev)))
+    mlp = mj.W8MLP(mk(I, K, 90), mk(I, K, 91), mk(H, I, 92))
+    x = torch.empty((1, K), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((1, I), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+
+    def fill(seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        x.copy_(torch.randn(x.shape, generator=g, device=dev).to(torch.bfloat16))
+
+    fill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mlp.forward(x, h, y)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        mlp.forward(x, h, y)
+    torch.cuda.synchronize()
+    assert graph_nodes(graph) == 2
+    graph.instantiate()
+    for rep in range(3):
+        fill(rep + 1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (bf16_host_bits(h), bf16_host_bits(y))
+        mlp.forward(x, h, y)
+        torch.cuda.synchronize()
+        want = (bf16_host_bits(h), bf16_host_bits(y))
+        np.testing.assert_array_equal(got[0], want[0], err_msg=f"replay {rep}: h")
+        np.testing.assert_array_equal(got[1], want[1], err_msg=f"replay {rep}: y")
+        assert np.any(got[1] != 0)

@@ -285,7 +285,8 @@ def test_c3_gemv(oracle, dev):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16, 17, 32])
-@pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16), (17, 48)])
+@pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16), (17, 48),
+                                 (130, 11008), (48, 6160)])
 def test_gemv_shapes(oracle, dev, M, N, K):
     x, Q, s, b = _w8_case(oracle, dev, M, N, K, M * 100 + N)
     for bias, epi in ((b, mj.EPI_NONE), (None, mj.EPI_GELU_TANH), (b, mj.EPI_SILU)):
@@ -364,7 +365,25 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    (1, 37, 4096), (1, 2000, 4096), (1, 3000, 4096),
                                    (1, 5000, 4096), (1, 11008, 4096), (1, 16001, 4096),
                                    (1, 16200, 4096),
-                                   (1, 37, 80), (1, 4104, 2064)])
+                                   (1, 37, 80), (1, 4104, 2064),
+                                   # M = 1, 4096 < K <= 16384: the K-split GEMV
+                                   # at 2, 3 and 4 chunks per lane (a partial
+                                   # last chunk round at K = 4112 and 12304),
+                                   # 4 to 48 rows per workgroup, grids of one
+                                   # to several rounds over the 256 CUs
+                                   (1, 5, 4112), (1, 37, 5008), (1, 3000, 8192),
+                                   (1, 20000, 6000), (1, 4096, 11008), (1, 9000, 12288),
+                                   (1, 100, 12304), (1, 13000, 16384),
+                                   # 2-4 x rows, K <= 16384: the two- and
+                                   # four-row K-split GEMVs (1-4 chunks per lane)
+                                   (2, 4096, 11008), (2, 20000, 6000), (2, 11008, 4096),
+                                   (3, 4096, 11008), (4, 37, 5008), (4, 1000, 16384),
+                                   (4, 300, 1040),
+                                   # 5-16 x rows, 4096 < K <= 16384: the long-K
+                                   # skinny MFMA GEMV, 2-4 passes (the last one
+                                   # 1-4 KB and past K), partial tiles
+                                   (5, 300, 5008), (9, 37, 12304), (16, 4100, 8192),
+                                   (16, 1000, 16384)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
@@ -493,7 +512,20 @@ def test_c5_mlp(oracle, dev):
 @pytest.mark.parametrize("M,K,I", [(512, 1024, 2000),   # 2 row tiles, partial last column tile
                                    (300, 528, 400),     # partial row tile, K % 64 != 0
                                    (1024, 256, 4096),   # 4 x 43 tiles, one K slice of 4 stages
-                                   (257, 64, 112)])     # one-row second tile, one stage
+                                   (257, 64, 112),      # one-row second tile, one stage
+                                   # one x row: the gate/up K-split GEMV at 1-4
+                                   # chunks per lane, 8 to 88 rows per workgroup
+                                   (1, 4096, 11008), (1, 1040, 400), (1, 6000, 304),
+                                   (1, 9008, 12000), (1, 16384, 3008),
+                                   # 2-4 x rows: the two- and four-row K-split
+                                   # GEMVs' gate/up
+                                   (2, 4096, 11008), (2, 1040, 400), (3, 5008, 304),
+                                   (4, 12288, 1008),
+                                   # 3-32 x rows at K = 1024 j: the skinny MFMA
+                                   # GEMV's gate/up tile pairs, one and two
+                                   # x-row groups, a partial last column tile
+                                   (3, 1024, 400), (16, 4096, 11008), (20, 2048, 1008),
+                                   (32, 3072, 112)])
 def test_mlp_gateup_integer_sums(oracle, dev, M, K, I):
     """The gate/up GEMM on exact sums: small-integer x, int8 weights and
     power-of-two scales make g = x Wg^T sg and u = x Wu^T su exact in fp32, so
@@ -523,7 +555,20 @@ def test_mlp_gateup_integer_sums(oracle, dev, M, K, I):
 
 @pytest.mark.parametrize("M,K,I,H", [(4, 256, 384, 128), (12, 256, 400, 130), (40, 512, 256, 320), (300, 256, 528, 64),
                                      # gate/up on 192-row tiles (a partial one), K % 64 != 0
-                                     (384, 1040, 400, 272)])
+                                     (384, 1040, 400, 272),
+                                     # one x row: the gate/up GEMV, then the down
+                                     # GEMV at K = I (the K-split one past 4096)
+                                     (1, 256, 384, 128), (1, 4096, 11008, 4096),
+                                     (1, 5008, 304, 272), (1, 1040, 12304, 100),
+                                     # 2-4 x rows: the K-split GEMVs for both
+                                     # projections; 5-32 at K = 1024 j: the
+                                     # gate/up on the skinny MFMA GEMV
+                                     (2, 1024, 400, 130), (2, 4096, 11008, 4096),
+                                     (4, 4096, 11008, 4096), (3, 1040, 304, 64),
+                                     (5, 2048, 1008, 272), (16, 4096, 11008, 4096),
+                                     (17, 3072, 304, 64), (32, 1024, 48, 16),
+                                     # gate/up GEMV, down on the GEMM
+                                     (24, 2048, 1008, 272)])
 def test_mlp_shapes(oracle, dev, M, K, I, H):
     case = _mlp_case(oracle, M, K, I, H, M)
     y, h = _run_mlp(dev, *case)
