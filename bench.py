@@ -67,7 +67,7 @@ def _args():
                    help="seconds of untimed load after the warmup launches of each workload")
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--only", default="", help="comma list of workloads (c1,c2,c3,c3batch,c3pack,c4,c4w8a8,c5,"
-                   "qlinear,bwd,conv2d,f64,copy,vendor); copy and vendor are run only when named")
+                   "c5decode,qlinear,bwd,conv2d,f64,copy,vendor); copy and vendor are run only when named")
     return p.parse_args()
 
 
@@ -258,6 +258,46 @@ def bench_c3_batch(steps, warmup):
                          "frac": gbs / PEAK_HBM_GBS, "traffic": None},
             "bytes_per_launch": bytes_,
             "timing": "graph replay of 64 launches rotating over 8 weight copies (> MALL)",
+        })
+    return out
+
+
+def bench_c5_decode(steps, warmup):
+    """The C5 FFN (4096 -> 11008 -> 4096, W8A16) at decode sizes, 1, 4 and 16
+    x rows: the gate/up GEMV and the down GEMV, HBM-bound on the 135 MB of
+    weights.  Graph replay rotating over 3 weight sets (405 MB > the MALL)."""
+    import torch
+    import momijo_amd as mj
+    K, I, H = 4096, 11008, 4096
+    copies = 3
+
+    def lin(n, k, seed):
+        W = _rand_f32((n, k), seed, 0.02)
+        q, s = mj.quantize_rowwise_int8(W)
+        del W
+        return mj.W8Linear(q, s)
+
+    mlps = [mj.W8MLP(lin(I, K, 60 + 3 * c), lin(I, K, 61 + 3 * c), lin(H, I, 62 + 3 * c))
+            for c in range(copies)]
+    out = []
+    for M in (1, 4, 16):
+        x = _rand_bf16((M, K), 70 + M)
+        h = torch.empty((M, I), dtype=torch.bfloat16, device="cuda")
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        ms = _graph_ms_per_launch(lambda i: mlps[i % copies].forward(x, h, y), 48,
+                                  max(max(steps, 400) // 48, 4))
+        # weights and scales of the three projections, x, h written and read, y
+        bytes_ = (3 * I * K + (2 * I + H) * 4 + M * K * 2 + 2 * M * I * 2 + M * H * 2)
+        gbs = bytes_ / (ms * 1e-3) / 1e9
+        out.append({
+            "name": f"c5decode_ffn_w8a16_m{M}",
+            "metric": f"W8A16 FFN 4096-11008-4096 GB/s (M={M})",
+            "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+            "bytes_per_launch": bytes_,
+            "timing": "graph replay of 48 FFN calls (two GEMV launches each) rotating over "
+                      "3 weight sets (> MALL)",
         })
     return out
 
@@ -715,7 +755,8 @@ def main():
     secondary = []
     for key, fn in (("c3", bench_c3), ("c3batch", bench_c3_batch), ("c3pack", bench_c3_pack),
                     ("c4", bench_c4),
-                    ("c4w8a8", bench_c4_w8a8), ("c5", bench_c5), ("qlinear", bench_qlinear), ("c1", bench_c1),
+                    ("c4w8a8", bench_c4_w8a8), ("c5", bench_c5), ("c5decode", bench_c5_decode),
+                    ("qlinear", bench_qlinear), ("c1", bench_c1),
                     ("bwd", bench_backward), ("conv2d", bench_conv2d),
                     ("f64", bench_f64), ("copy", bench_copy), ("vendor", bench_vendor)):
         if want(key) and (key not in ("copy", "vendor") or key in only):
