@@ -284,9 +284,10 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
 // forms bf16(silu(g sg) (u su)) from the two fp32 tile sums): the weights
 // stream as whole row pieces and reach the MFMA through LDS.  NWV waves split
 // K (KQ = K / NWV bytes of every row each); a workgroup owns 16 TILES weight
-// rows.  For each 16-row tile a wave copies its share of the 16 rows straight
-// into its own LDS region (buffer_load ... lds, 1 KB per instruction: 1024 /
-// KQ rows of KQ contiguous bytes), two tiles in flight, then reads the MFMA
+// rows.  For each 16-row tile a wave copies its share of the 16 rows into its
+// own LDS region, 1 KB per instruction (1024 / KQ rows of KQ contiguous bytes):
+// with REG through registers (buffer loads, then ds_write once they landed),
+// else straight (buffer_load ... lds); two tiles in flight.  It then reads the MFMA
 // fragments from there: lane (r, c) takes 16 int8 of row r at 16-byte chunk
 // 4 j + c of 64-deep block j, widened exactly to bf16, the first 8 k for one
 // v_mfma_f32_16x16x32_bf16 and the other 8 for the second, against x
@@ -304,7 +305,10 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
 // waves, 10.8 with eight; the rest is the widening (1.5 VALU per weight).
 // Refilling a slot as soon as its fragments are in registers (two tiles in
 // flight during the compute) measured slower, and a third slot does not fit
-// the LDS.
+// the LDS.  Through registers (REG) the same launches take 12.2, 12.3, 13.8
+// us at M = 3, 8, 16 (alternating runs on one box: 13.4, 13.6, 15.4 straight
+// into LDS); with two x groups (232-248 VGPRs) they take 1 us longer, so M
+// > 16 copies straight.
 __device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void *)lds_dst, 16, off, 0, 0, 2 /* nt */);
@@ -313,7 +317,7 @@ __device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_ds
 // s_waitcnt immediate: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F70; }
 
-template <int TILES, int KB, int NWV, int MB, bool GATEUP>
+template <int TILES, int KB, int NWV, int MB, bool GATEUP, bool REG = false>
 __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
     const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
     const float *__restrict__ scales, const float *__restrict__ scales2,
@@ -360,6 +364,10 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
   // tile t's share -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
   // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7).
   // GATEUP: tile 2 j is gate rows 16 j.., tile 2 j + 1 the up rows of the same columns
+  // tiles in flight (three, with registers for them, measured 0.6-0.8 us slower
+  // at 3-16 x rows)
+  constexpr int DEPTH = 2;
+  uint4 R[DEPTH][REG ? ninst : 1];
   auto issue = [&](int t) {
     uint8_t *dst = mine + (t & 1) * SLOT;
     const int tr = GATEUP ? t >> 1 : t;
@@ -368,18 +376,34 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
       const int e = 1024 * i + 16 * lane;
       const int rr = e / KQ, p = (e - rr * KQ) >> 4;
       const uint32_t off = (uint32_t)((tr * 16 + rr) * K + kq0 + 16 * (p ^ (rr & 7)));
-      dma16_lds((GATEUP && (t & 1)) ? rQ2 : rQ, dst + 1024 * i, off);
+      if constexpr (REG) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (t & 1)) ? rQ2 : rQ,
+                                                              off, 0, 2 /* nt */);
+        R[t % DEPTH][i] = make_uint4(v[0], v[1], v[2], v[3]);
+      } else {
+        dma16_lds((GATEUP && (t & 1)) ? rQ2 : rQ, dst + 1024 * i, off);
+      }
     }
   };
-  issue(0);
-  if (TILES > 1) issue(1);
+#pragma unroll
+  for (int t = 0; t < DEPTH; ++t)
+    if (t < TILES) issue(t);
   f32x4 acc[TILES][MB];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
-    // tile t landed: at most the copies of tile t + 1 still outstanding
-    if (t + 1 < TILES) __builtin_amdgcn_s_waitcnt(vmcnt_imm(ninst));
+    // tile t landed: at most the loads of the next DEPTH - 1 tiles outstanding
+    const int later = TILES - 1 - t < DEPTH - 1 ? TILES - 1 - t : DEPTH - 1;
+    if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * ninst));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(ninst));
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     asm volatile("" ::: "memory");
+    if constexpr (REG) {
+#pragma unroll
+      for (int i = 0; i < ninst; ++i)
+        *(uint4 *)(mine + (t & 1) * SLOT + 1024 * i + 16 * lane) = R[t % DEPTH][i];
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+    }
     const uint8_t *src = mine + (t & 1) * SLOT + r * KQ;
     // two independent accumulator chains per x group (the chunk halves), added
     // in a fixed order at the end
@@ -406,11 +430,11 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
     }
 #pragma unroll
     for (int g = 0; g < MB; ++g) acc[t][g] = ch[g][0] + ch[g][1];
-    if (t + 2 < TILES) {
+    if (t + DEPTH < TILES) {
       // this wave's fragment reads of the slot are done before it is refilled
       __builtin_amdgcn_s_waitcnt(0xC07F);
       asm volatile("" ::: "memory");
-      issue(t + 2);
+      issue(t + DEPTH);
     }
   }
   // every wave is past its last fragment read (and its copies have landed):
@@ -464,14 +488,14 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
   }
 }
 
-template <int TILES, int KB, int NWV, int MB, bool GATEUP>
+template <int TILES, int KB, int NWV, int MB, bool GATEUP, bool REG>
 static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
                                   const float *scales, const float *scales2, const float *bias,
                                   int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
                                   hipStream_t stream) {
   constexpr size_t lds = 2 * 65536;
   static_assert(NWV * TILES * MB * 64 * sizeof(f32x4) <= lds, "partials fit the slots");
-  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB, GATEUP>;
+  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB, GATEUP, REG>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -493,11 +517,14 @@ static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t
                                 const float *scales, const float *scales2, const float *bias,
                                 int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
                                 hipStream_t stream) {
+  // one x group: the weights through registers; two (232-248 VGPRs): straight
+  // into LDS (the register path measured 1 us slower there)
+  constexpr bool REG = MB == 1;
   switch (K / 512) {
 #define MJ_SK(kb)                                                                             \
   case kb:                                                                                    \
-    return launch_skinny_k<TILES, kb, NWV, MB, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, \
-                                                       M, N, K, stream);
+    return launch_skinny_k<TILES, kb, NWV, MB, GATEUP, REG>(x, Q, Q2, scales, scales2, bias,  \
+                                                            epi, y, M, N, K, stream);
     MJ_SK(2) MJ_SK(4) MJ_SK(6) MJ_SK(8)
 #undef MJ_SK
     default: return hipErrorInvalidValue;
@@ -509,7 +536,8 @@ static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t
 // last one of 512 KBL bytes that covers the rest (K rounded up to 1024).  A
 // step is one (pass, tile) pair, passes outermost: each wave copies its
 // 4096 / NWV-byte (last pass 64 KBL) share of the tile's 16 rows into its own
-// LDS slot exactly as the K <= 4096 kernel does (two steps in flight), and
+// LDS slot through registers as the K <= 4096 kernel does with REG (two steps
+// in flight; 1.0-1.3 us faster at M = 5-16 than copies straight into LDS), and
 // multiplies it against the x fragments of that pass, which sit in one of two
 // register sets: the next pass's x loads are issued just before its first
 // copy, so the wait for that copy also covers them, while the current pass
@@ -562,10 +590,10 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_long_kernel(
   constexpr int kCopiesF = KQF / 64, kCopiesL = KQL / 64;
   constexpr int kXLoadsF = 2 * kCopiesF, kXLoadsL = 2 * kCopiesL;
   // step st = (pass p, tile t) -> slot st & 1, as the K <= 4096 kernel's copies
+  uint4 R[2][KQF / 64];
   auto issue = [&](int st) {
     const int p = st / TILES, t = st % TILES;
     const int KQ = p + 1 < NP ? KQF : KQL;
-    uint8_t *dst = mine + (st & 1) * SLOT;
 #pragma unroll
     for (int i = 0; i < KQF / 64; ++i) {
       if (i < KQ / 64) {
@@ -573,7 +601,8 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_long_kernel(
         const int rr = e / KQ, ch = (e - rr * KQ) >> 4;
         const uint32_t off =
             (uint32_t)((t * 16 + rr) * K + 4096 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
-        dma16_lds(rQ, dst + 1024 * i, off);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rQ, off, 0, 2 /* nt */);
+        R[st & 1][i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     }
   };
@@ -601,6 +630,11 @@ __global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_long_kernel(
     } else {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < KQF / 64; ++i)
+      if (i < KQ / 64) *(uint4 *)(mine + (st & 1) * SLOT + 1024 * i + 16 * lane) = R[st & 1][i];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("" ::: "memory");
     const uint8_t *src = mine + (st & 1) * SLOT + r * KQ;
     f32x4 ch0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, ch1 = ch0;
