@@ -211,9 +211,10 @@ def test_sweep_f32_matmul(dev, M, N, K, ta, tb):
 # K = 16384 for as long as asked, over the W8A16 Linear, the bf16 GEMM, the
 # int8 GEMM and the fp32 matmul (with transposed views), every output compared
 # with exact float64 products (small-integer operands, power-of-two scales)
-# rounded by the oracle's pinned bf16 rounding; and over the two quantizers
+# rounded by the oracle's pinned bf16 rounding; over the two quantizers
 # (per-row RHE / legacy with exact-tie rows, per-tensor legacy with
-# near-ties), bit for bit against the oracle.
+# near-ties), bit for bit against the oracle; and over the W8A16 FFN (decode
+# and prefill sizes) against float64 bounds.
 _LONG = float(os.environ.get("MJ_LONG_SWEEP", "0"))
 
 
@@ -293,6 +294,41 @@ def _long_case(rng, fam, dev, to_bf16, oracle_quantize_rowwise=None, oracle_quan
                      rng.standard_normal(n + off) * 100 * sv).astype(np.float32)
         got = mj.quantize_symmetric_int8(mj.Tensor(to_dev(x, dev)[off:]), float(sv)).numpy()
         return (fam, n, off, float(sv)), got, oracle_quantize_tensor(x[off:], sv)
+    elif fam == "mlp":
+        # the FFN over its GEMV and GEMM paths: 1, 2-4, 5-16, 17-32 or 33-600 x
+        # rows, K up to 16384 (a third of the cases K = 1024 j <= 4096), exact
+        # gate/up sums; h within one bf16 step of the float64 value from them,
+        # y within one bf16 step plus 2^-16 of the sum of |h Wd| (fp32 summation)
+        M = [1, int(rng.integers(2, 5)), int(rng.integers(5, 17)), int(rng.integers(17, 33)),
+             int(rng.integers(33, 601))][rng.integers(0, 5)]
+        K = int(rng.integers(1, 5)) * 1024 if rng.integers(0, 3) == 0 else \
+            int(rng.integers(1, 1025)) * 16
+        I, H = int(rng.integers(1, 751)) * 16, int(rng.integers(1, 4097))
+        while (M * (2 * I * K + H * I) > 6e9 or 2 * I * K + H * I > 1.5e8) and (K > 16 or I > 16):
+            if K >= I:
+                K = max(16, (K // 2) // 16 * 16)
+            else:
+                I = max(16, (I // 2) // 16 * 16)
+        x = rng.integers(-4, 5, size=(M, K)).astype(np.float32)
+        Wg = rng.integers(-127, 128, size=(I, K), dtype=np.int8)
+        Wu = rng.integers(-127, 128, size=(I, K), dtype=np.int8)
+        Wd = rng.integers(-127, 128, size=(H, I), dtype=np.int8)
+        sg = (2.0 ** rng.integers(-14, -10, size=I)).astype(np.float32)
+        su = (2.0 ** rng.integers(-14, -10, size=I)).astype(np.float32)
+        sd = (2.0 ** rng.integers(-12, -8, size=H)).astype(np.float32)
+        mk = lambda q, sc: mj.W8Linear(to_dev(q, dev), to_dev(sc, dev))  # noqa: E731
+        y, h = mj.W8MLP(mk(Wg, sg), mk(Wu, su), mk(Wd, sd)).forward(bf16_dev(to_bf16(x), dev))
+        h, y = bf16_host_f32(h).astype(np.float64), bf16_host_f32(y).astype(np.float64)
+        xf = x.astype(np.float64)
+        g = (xf @ Wg.astype(np.float64).T) * sg.astype(np.float64)
+        u = (xf @ Wu.astype(np.float64).T) * su.astype(np.float64)
+        href = g / (1.0 + np.exp(-g)) * u
+        hbad = np.abs(h - href) > np.maximum(np.abs(href) * 2.0 ** -8, 1e-6)
+        Wdf = Wd.astype(np.float64)
+        yref = (h @ Wdf.T) * sd.astype(np.float64)
+        ybound = np.abs(yref) * 2.0 ** -8 + 2.0 ** -16 * (np.abs(h) @ np.abs(Wdf).T) * sd + 1e-30
+        ybad = np.abs(y - yref) > ybound
+        return (fam, M, K, I, H), np.array([int(hbad.sum()), int(ybad.sum())]), np.array([0, 0])
     else:
         M, N, K = (int(v) for v in rng.integers(1, 3000, size=3))
         ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
@@ -307,7 +343,7 @@ def _long_case(rng, fam, dev, to_bf16, oracle_quantize_rowwise=None, oracle_quan
 def test_long_random_sweep(oracle, dev):
     rng = np.random.default_rng(int(os.environ.get("MJ_LONG_SWEEP_SEED", "7")))
     t_end, n, bad = time.time() + _LONG, 0, []
-    fams = ("w8a16", "bf16", "i8", "f32", "qrow", "qtensor")
+    fams = ("w8a16", "bf16", "i8", "f32", "qrow", "qtensor", "mlp")
     qrow = lambda W, r: oracle.quantize_rowwise_rhe(W) if r == mj.ROUND_RHE else \
         oracle.quantize_rowwise_legacy(W)  # noqa: E731
     while time.time() < t_end:
