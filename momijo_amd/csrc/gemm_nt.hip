@@ -1915,8 +1915,8 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
                        p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
   if (p.gate_up) {
-    // output columns per tile are BN/2: 128 at BN = 256 (the 8-wave kernel
-    // for M <= 128 takes only that), 96 at BN = 192 on the tile kernel below.
+    // output columns per tile are BN/2: 64 at BN = 128 (M <= 128, below), 96
+    // at BN = 192 or 128 at BN = 256 on the tile kernel.
     // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
     // and up: 20 us faster than the 8-wave kernel) in its split layout: 1 x 4
     // waves of 256 x BN/4, gate rows in waves 0-1 and the up rows of the same
@@ -1925,8 +1925,15 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // each pairing its own gate and up blocks): bit-identical, C5's gate/up
     // 78.6 -> 68.1 us, 1024 x 4096 x 4096 73.7 -> 61.2 us (MI355X, settled A/B
     // in one process)
-    pl.bm = p.M > 128 ? 256 : 128;
-    pl.bn = 256;
+    // M <= 128 (past the gate/up GEMV): 64 output columns per tile on four
+    // waves (one per SIMD, 2 x 2 of BM/2 x 64), 64 rows for M <= 64, so the
+    // grid has 172 workgroups at I = 11008 instead of 86 on 128 x 256 tiles
+    // of eight waves.  The FFN 4096 -> 11008 -> 4096 at M = 33 / 64 / 96 /
+    // 128 (MI355X, one box): 96.6 / 97.3 / 99.2 / 102.3 us -> 79.6 / 80.4 /
+    // 91.6 / 94.4 us; 32 output columns on two waves (344 workgroups) 85.9 /
+    // 85.5 / 98.1 / 100.6 us
+    pl.bm = p.M > 128 ? 256 : p.M > 64 ? 128 : 64;
+    pl.bn = p.M > 128 ? 256 : 128;
     pl.tile_kernel = pl.bm == 256 && w4i8_ok;
     if (pl.tile_kernel) {
       pl.wm = 256;
@@ -2019,6 +2026,10 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
       return hipErrorInvalidValue;
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
+    if (pl.bn == 128) {
+      if (pl.bm == 64) return launch_tile<64, 128, B_INT8, true, false, false, 4>(p, stream);
+      return launch_tile<128, 128, B_INT8, true, false, false, 4>(p, stream);
+    }
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
   }
   if (pl.splits > 1 && p.part == nullptr) return hipErrorInvalidValue;

@@ -517,6 +517,8 @@ def test_c5_mlp(oracle, dev):
                                    # chunks per lane, 8 to 88 rows per workgroup
                                    (1, 4096, 11008), (1, 1040, 400), (1, 6000, 304),
                                    (1, 9008, 12000), (1, 16384, 3008),
+                                   # 33-128 x rows: the gate/up GEMM's narrow tiles
+                                   (33, 1024, 1008), (64, 4096, 11008), (128, 1040, 720),
                                    # 2-4 x rows: the two- and four-row K-split
                                    # GEMVs' gate/up
                                    (2, 4096, 11008), (2, 1040, 400), (3, 5008, 304),
@@ -568,7 +570,11 @@ def test_mlp_gateup_integer_sums(oracle, dev, M, K, I):
                                      (5, 2048, 1008, 272), (16, 4096, 11008, 4096),
                                      (17, 3072, 304, 64), (32, 1024, 48, 16),
                                      # gate/up GEMV, down on the GEMM
-                                     (24, 2048, 1008, 272)])
+                                     (24, 2048, 1008, 272),
+                                     # 33-128 x rows: the gate/up GEMM's narrow
+                                     # tiles (a partial last one), down GEMM
+                                     (33, 1024, 1008, 272), (64, 4096, 11008, 512),
+                                     (100, 2048, 400, 64), (128, 1040, 720, 130)])
 def test_mlp_shapes(oracle, dev, M, K, I, H):
     case = _mlp_case(oracle, M, K, I, H, M)
     y, h = _run_mlp(dev, *case)
