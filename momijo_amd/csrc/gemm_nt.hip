@@ -1915,8 +1915,9 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
                        p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
   if (p.gate_up) {
-    // output columns per tile are BN/2: 64 at BN = 128 (M <= 128, below), 96
-    // at BN = 192 or 128 at BN = 256 on the tile kernel.
+    // output columns per tile are BN/2: 64, 96 or 128 on the tile kernel
+    // below, 128 on the 8-wave kernel (the fallback for weights past 31-bit
+    // offsets or K >= 2^30).
     // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
     // and up: 20 us faster than the 8-wave kernel) in its split layout: 1 x 4
     // waves of 256 x BN/4, gate rows in waves 0-1 and the up rows of the same
@@ -1925,24 +1926,29 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     // each pairing its own gate and up blocks): bit-identical, C5's gate/up
     // 78.6 -> 68.1 us, 1024 x 4096 x 4096 73.7 -> 61.2 us (MI355X, settled A/B
     // in one process)
-    // M <= 128 (past the gate/up GEMV): 64 output columns per tile on four
-    // waves (one per SIMD, 2 x 2 of BM/2 x 64), 64 rows for M <= 64, so the
-    // grid has 172 workgroups at I = 11008 instead of 86 on 128 x 256 tiles
-    // of eight waves.  The FFN 4096 -> 11008 -> 4096 at M = 33 / 64 / 96 /
-    // 128 (MI355X, one box): 96.6 / 97.3 / 99.2 / 102.3 us -> 79.6 / 80.4 /
-    // 91.6 / 94.4 us; 32 output columns on two waves (344 workgroups) 85.9 /
-    // 85.5 / 98.1 / 100.6 us
-    pl.bm = p.M > 128 ? 256 : p.M > 64 ? 128 : 64;
-    pl.bn = p.M > 128 ? 256 : 128;
-    pl.tile_kernel = pl.bm == 256 && w4i8_ok;
+    //
+    // Any M goes to the tile kernel (256-row tiles, rows past M loading
+    // zeros), its B rows per tile (gate and up: 2 x the output columns) the
+    // fewest columns per CU: rounds of 256 workgroups times columns per
+    // workgroup, over 64, 96 and 128 columns, ties to the wider tile.  At M
+    // <= 256 and I = 11008 that is 64 columns, 172 workgroups: the FFN 4096 ->
+    // 11008 -> 4096 (MI355X) at M = 33 / 64 / 128 / 192 / 256 took 80.2 /
+    // 80.6 / 94.9 / 98.1 / 103.5 us with the gate/up on 96- or 128-column
+    // tiles (the 8-wave kernel's 64 x 128 or 128 x 128 tiles of four waves up
+    // to 128 rows), 73.2-74.3 / 72.8 / 75.6 / 86.2-86.7 / 90.8-91.1 us here;
+    // M = 512 keeps 96 columns (230 workgroups).
+    pl.bm = p.M > 128 || w4i8_ok ? 256 : 128;
+    pl.bn = 256;
+    pl.tile_kernel = w4i8_ok;
     if (pl.tile_kernel) {
       pl.wm = 256;
-      // 192 B rows (96 output columns) when that runs fewer columns per CU:
-      // rounds of 256 workgroups times columns per workgroup
       const int64_t tm = (p.M + 255) / 256;
       const int64_t r256 = (tm * ((p.N + 127) / 128) + 255) / 256;
       const int64_t r192 = (tm * ((p.N + 95) / 96) + 255) / 256;
-      if (r192 * 96 < r256 * 128) pl.bn = 192;
+      const int64_t r128 = (tm * ((p.N + 63) / 64) + 255) / 256;
+      int64_t best = r256 * 128;
+      if (r192 * 96 < best) pl.bn = 192, best = r192 * 96;
+      if (r128 * 64 < best) pl.bn = 128;
     }
     return pl;
   }
@@ -2021,15 +2027,12 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.tile_kernel) {
       if (pl.bm != 256 || pl.wm != 256) return hipErrorInvalidValue;
+      if (pl.bn == 128) return launch_w4i8<256, 128, true, 256>(p, stream);
       if (pl.bn == 192) return launch_w4i8<256, 192, true, 256>(p, stream);
       if (pl.bn == 256) return launch_w4i8<256, 256, true, 256>(p, stream);
       return hipErrorInvalidValue;
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
-    if (pl.bn == 128) {
-      if (pl.bm == 64) return launch_tile<64, 128, B_INT8, true, false, false, 4>(p, stream);
-      return launch_tile<128, 128, B_INT8, true, false, false, 4>(p, stream);
-    }
     return launch_tile<128, 256, B_INT8, true, false>(p, stream);
   }
   if (pl.splits > 1 && p.part == nullptr) return hipErrorInvalidValue;

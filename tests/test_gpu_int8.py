@@ -519,6 +519,7 @@ def test_c5_mlp(oracle, dev):
                                    (1, 9008, 12000), (1, 16384, 3008),
                                    # 33-128 x rows: the gate/up GEMM's narrow tiles
                                    (33, 1024, 1008), (64, 4096, 11008), (128, 1040, 720),
+                                   (200, 1024, 2000), (256, 4096, 11008),
                                    # 2-4 x rows: the two- and four-row K-split
                                    # GEMVs' gate/up
                                    (2, 4096, 11008), (2, 1040, 400), (3, 5008, 304),
@@ -574,7 +575,9 @@ def test_mlp_gateup_integer_sums(oracle, dev, M, K, I):
                                      # 33-128 x rows: the gate/up GEMM's narrow
                                      # tiles (a partial last one), down GEMM
                                      (33, 1024, 1008, 272), (64, 4096, 11008, 512),
-                                     (100, 2048, 400, 64), (128, 1040, 720, 130)])
+                                     (100, 2048, 400, 64), (128, 1040, 720, 130),
+                                     # 129-256 x rows on 64-column gate/up tiles
+                                     (200, 1024, 2000, 272), (256, 4096, 11008, 256)])
 def test_mlp_shapes(oracle, dev, M, K, I, H):
     case = _mlp_case(oracle, M, K, I, H, M)
     y, h = _run_mlp(dev, *case)
