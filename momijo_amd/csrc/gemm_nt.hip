@@ -1265,6 +1265,7 @@ __device__ __forceinline__ void gateup_split_epilogue(const GemmNT &p, const f32
                                                       float *xs, int m0, int n0, int wn, int lane,
                                                       bool full) {
   constexpr int HM = TM / 2;            // row blocks handed over / kept
+  constexpr int HR = HM * 16;           // rows of one exchange region
   constexpr int LDX = 2 * WN + 4;       // fp32 row stride of the exchange regions
   const int N = (int)p.N;
   const int fr = lane & 15, fh = lane >> 4;
@@ -1295,14 +1296,14 @@ __device__ __forceinline__ void gateup_split_epilogue(const GemmNT &p, const f32
 #pragma clang fp contract(off)
           v[q] = acc[send0 + i][j][q] * sc[j][q];
         }
-        *(f32x4 *)(xs + ((UP ? 128 : 0) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh) = v;
+        *(f32x4 *)(xs + ((UP ? HR : 0) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh) = v;
       }
     __syncthreads();
     // h of row block keep0 + i, column block j (4 values of one lane), the
     // partner's half from the other region
     auto h4 = [&](int i, int j, float (&h)[4]) {
       const f32x4 o =
-          *(const f32x4 *)(xs + ((UP ? 0 : 128) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh);
+          *(const f32x4 *)(xs + ((UP ? 0 : HR) + i * 16 + fr) * LDX + cw + j * 16 + 4 * fh);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma clang fp contract(off)
@@ -1378,7 +1379,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   // BN/2 up rows of the same output columns, so waves 0-1 hold gate sums and
   // waves 2-3 the up sums of the same columns (paired in the epilogue through
   // LDS)
-  static_assert(!GATEUP || WMT == 256, "gate/up runs the split layout");
+  static_assert(!GATEUP || WMS == 1, "gate/up runs the split layout (1 x 4 waves)");
   static_assert(TN >= 2, "the widened-fragment rotation needs two blocks per step");
   // the B widening of a group sits beside its last 8 MFMAs
   constexpr int CU0 = TM - 8;
@@ -1819,7 +1820,7 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr size_t lds_loop = size_t(2) * BM * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
   constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
   // the split gate/up epilogue's two fp32 exchange regions (128 rows each)
-  constexpr size_t lds_x = (GATEUP && WMT == 256) ? size_t(2) * 128 * (BN_OUT + 4) * 4 : 0;
+  constexpr size_t lds_x = GATEUP ? size_t(2) * (WMT / 2) * (BN_OUT + 4) * 4 : 0;
   constexpr size_t lds_lo = lds_loop > lds_out ? lds_loop : lds_out;
   constexpr size_t lds = lds_lo > lds_x ? lds_lo : lds_x;
   static_assert(lds <= 160 * 1024, "LDS budget");
@@ -1915,33 +1916,26 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
                        p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
   if (p.gate_up) {
-    // output columns per tile are BN/2: 64, 96 or 128 on the tile kernel
-    // below, 128 on the 8-wave kernel (the fallback for weights past 31-bit
-    // offsets or K >= 2^30).
-    // M > 128 runs the one-wave-per-SIMD int8 kernel (512 x 22016 x 4096 gate
-    // and up: 20 us faster than the 8-wave kernel) in its split layout: 1 x 4
-    // waves of 256 x BN/4, gate rows in waves 0-1 and the up rows of the same
-    // columns in waves 2-3, paired through LDS in the epilogue.  A widened
-    // fragment then feeds 16 MFMAs instead of 8 (2 x 2 waves of 128 x BN/2,
-    // each pairing its own gate and up blocks): bit-identical, C5's gate/up
-    // 78.6 -> 68.1 us, 1024 x 4096 x 4096 73.7 -> 61.2 us (MI355X, settled A/B
-    // in one process)
-    //
-    // Any M goes to the tile kernel (256-row tiles, rows past M loading
-    // zeros), its B rows per tile (gate and up: 2 x the output columns) the
-    // fewest columns per CU: rounds of 256 workgroups times columns per
-    // workgroup, over 64, 96 and 128 columns, ties to the wider tile.  At M
-    // <= 256 and I = 11008 that is 64 columns, 172 workgroups: the FFN 4096 ->
-    // 11008 -> 4096 (MI355X) at M = 33 / 64 / 128 / 192 / 256 took 80.2 /
-    // 80.6 / 94.9 / 98.1 / 103.5 us with the gate/up on 96- or 128-column
-    // tiles (the 8-wave kernel's 64 x 128 or 128 x 128 tiles of four waves up
-    // to 128 rows), 73.2-74.3 / 72.8 / 75.6 / 86.2-86.7 / 90.8-91.1 us here;
-    // M = 512 keeps 96 columns (230 workgroups).
+    // The one-wave-per-SIMD int8 kernel in its split layout: 1 x 4 waves of
+    // BM x BN/4, gate rows in waves 0-1 and the up rows of the same columns
+    // in waves 2-3, paired through LDS in the epilogue (a widened fragment
+    // feeds 16 MFMAs; against 2 x 2 waves each pairing its own gate and up
+    // blocks C5's gate/up 78.6 -> 68.1 us; against the 8-wave kernel, which
+    // remains the fallback for weights past 31-bit offsets or K >= 2^30, 20
+    // us faster).  Tiles of 256 rows, 128 up to 128 rows (half the MFMAs on
+    // zero rows: the FFN 4096 -> 11008 -> 4096 at M = 33 / 64 / 128 73.9-75.2
+    // / 72.5-72.8 / 76.4-76.5 -> 63.5-63.7 / 63.6-63.8 / 68.0-68.2 us), rows
+    // past M loading zeros.  Output columns per tile (BN/2): 64, 96 or 128,
+    // the fewest columns per CU (rounds of 256 workgroups times columns), ties
+    // to the wider tile: 64 (172 workgroups) at I = 11008 up to 256 rows, 96
+    // (230) at 512.  The 64-column tiles against 96 / 128 took the FFN at M =
+    // 192 / 256 from 98.1 / 103.5 to 86.2-86.7 / 90.8-91.1 us.
     pl.bm = p.M > 128 || w4i8_ok ? 256 : 128;
     pl.bn = 256;
     pl.tile_kernel = w4i8_ok;
     if (pl.tile_kernel) {
-      pl.wm = 256;
+      pl.wm = p.M <= 128 ? 128 : 256;
+      pl.bm = pl.wm;
       const int64_t tm = (p.M + 255) / 256;
       const int64_t r256 = (tm * ((p.N + 127) / 128) + 255) / 256;
       const int64_t r192 = (tm * ((p.N + 95) / 96) + 255) / 256;
@@ -2026,6 +2020,11 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     p.part = nullptr;
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.tile_kernel) {
+      if (pl.bm == 128 && pl.wm == 128) {
+        if (pl.bn == 128) return launch_w4i8<128, 128, true, 128>(p, stream);
+        if (pl.bn == 192) return launch_w4i8<128, 192, true, 128>(p, stream);
+        return launch_w4i8<128, 256, true, 128>(p, stream);
+      }
       if (pl.bm != 256 || pl.wm != 256) return hipErrorInvalidValue;
       if (pl.bn == 128) return launch_w4i8<256, 128, true, 256>(p, stream);
       if (pl.bn == 192) return launch_w4i8<256, 192, true, 256>(p, stream);
