@@ -897,6 +897,60 @@ __device__ __forceinline__ void store_w8a8(const GemmI8 &p, const i32x4 (&acc)[T
   }
 }
 
+// The W8A8 epilogue for a tile wholly inside the output with 16-byte aligned
+// rows: the values of store_w8a8 (same operations, same order), with blocks
+// j, j+1 exchanged through v_permlane16_swap so each lane stores 8
+// consecutive bf16 columns in one 16-byte store, the j pairs inner so both
+// halves of a 128-byte output line are written together (as
+// store_tile_direct does for the W8A16 kernels).
+template <int E, int TM, int TN, int WN>
+__device__ __forceinline__ void store_w8a8_direct(const GemmI8 &p, const i32x4 (&acc)[TM][TN],
+                                                  int m0, int n0, int wm, int wn, int lane) {
+  static_assert(TN % 2 == 0, "column blocks in pairs");
+  const int fr = lane & 15, fh = lane >> 4;
+  const bool has_b = p.bias != nullptr;
+  float swq[TN][4], bq[TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wn * WN + j * 16 + 4 * fh + q;
+      swq[j][q] = p.sw[n];
+      bq[j][q] = has_b ? p.bias[n] : 0.0f;
+    }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * 128 + i * 16 + fr;
+    const float sxm = p.sx[m];
+#pragma unroll
+    for (int j = 0; j < TN; j += 2) {
+      float x[4], y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t0, t1;
+        {
+#pragma clang fp contract(off)
+          const float sf0 = sxm * swq[j][q], sf1 = sxm * swq[j + 1][q];
+          t0 = (float)acc[i][j][q] * sf0;
+          t1 = (float)acc[i][j + 1][q] * sf1;
+          if (has_b) {
+            t0 = t0 + bq[j][q];
+            t1 = t1 + bq[j + 1][q];
+          }
+        }
+        x[q] = apply_epi_b16(E, t0);
+        y[q] = apply_epi_b16(E, t1);
+      }
+      const auto w0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[0], x[1]),
+                                                       pack_bf16x2(y[0], y[1]), false, false);
+      const auto w1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(x[2], x[3]),
+                                                       pack_bf16x2(y[2], y[3]), false, false);
+      const int n = n0 + wn * WN + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
+      *(uint4 *)(p.Yb + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
+    }
+  }
+}
+
 template <int BN, int MODE>
 __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   constexpr int BM = 256;
@@ -1062,6 +1116,22 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
   __syncthreads();
 
   if constexpr (MODE == 2) {
+    const bool full = m0 + BM <= M && n0 + BN <= N && (p.ldc & 7) == 0 &&
+                      ((uintptr_t)p.Yb & 15) == 0;
+    if (full) {
+      switch (p.epi) {
+#define MJ_W8A8D(E) store_w8a8_direct<E, TM, TN, WN>(p, acc, m0, n0, wm, wn, lane); break;
+        case EPI_RELU: MJ_W8A8D(EPI_RELU)
+        case EPI_GELU_TANH: MJ_W8A8D(EPI_GELU_TANH)
+        case EPI_SILU: MJ_W8A8D(EPI_SILU)
+        case EPI_GELU_TANH_APPROX: MJ_W8A8D(EPI_GELU_TANH_APPROX)
+        case EPI_SILU_APPROX: MJ_W8A8D(EPI_SILU_APPROX)
+        case EPI_RELU_UNARY: MJ_W8A8D(EPI_RELU_UNARY)
+        default: MJ_W8A8D(EPI_NONE)
+#undef MJ_W8A8D
+      }
+      return;
+    }
     switch (p.epi) {
 #define MJ_W8A8(E) store_w8a8<E, TM, TN, WN>(p, acc, m0, n0, wm, wn, lane); break;
       case EPI_RELU: MJ_W8A8(EPI_RELU)
@@ -1076,20 +1146,25 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
     return;
   }
   // a lane's block (i, j) holds output row m0 + wm*WM + 16 i + (lane & 15) at
-  // the 4 columns n0 + wn*WN + 16 j + 4 (lane >> 4) + q
+  // the 4 columns n0 + wn*WN + 16 j + 4 (lane >> 4) + q.  Blocks j of one
+  // row block go out back to back (j inner): consecutive 64-byte pieces of
+  // the same output rows, so whole 128-byte lines reach the L2 together.
   const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)(MODE == 0 ? (void *)p.C : (void *)p.Y) & 15) == 0;
+  float bq[TN][4];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int nb = n0 + wn * WN + j * 16 + 4 * fh;
-    float bq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (MODE == 1) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) bq[q] = p.bias ? p.bias[nb + q < N ? nb + q : N - 1] : 0.0f;
-    }
+    for (int q = 0; q < 4; ++q)
+      bq[j][q] = MODE == 1 && p.bias ? p.bias[nb + q < N ? nb + q : N - 1] : 0.0f;
+  }
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm * WM + i * 16 + fr;
-      if (m >= M) continue;
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WM + i * 16 + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int nb = n0 + wn * WN + j * 16 + 4 * fh;
       if constexpr (MODE == 0) {
         int32_t *dst = p.C + (size_t)m * p.ldc + nb;
         if (vec && nb + 3 < N) {
@@ -1104,7 +1179,7 @@ __global__ __launch_bounds__(256) void gemm_i8_w4_kernel(GemmI8 p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
 #pragma clang fp contract(off)
-          v[q] = (float)acc[i][j][q] * p.sf + bq[q];
+          v[q] = (float)acc[i][j][q] * p.sf + bq[j][q];
         }
         float *dst = p.Y + (size_t)m * p.ldc + nb;
         if (vec && nb + 3 < N) {
