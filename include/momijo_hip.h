@@ -319,7 +319,7 @@ int32_t mj_quantize_rowwise_i8(const float *W, int64_t N, int64_t K, int32_t rou
                                int8_t *Q, float *scales, void *stream);
 
 /* y[M,N] = bf16(epi((x[M,K] . Q[N,K]^T) * scales[N] + bias[N])) with x bf16,
- * fp32 accumulation.  M <= 16 (and M <= 32 when K is a multiple of 1024 up
+ * fp32 accumulation.  M <= 16 (and M <= 48 when K is a multiple of 1024 up
  * to 4096) runs the GEMV kernels, larger M the MFMA GEMM with int8 -> bf16
  * conversion in registers.  bias may be NULL.  Needs K % 16 == 0 and 16-byte
  * aligned x, Q, y. */

@@ -727,6 +727,193 @@ static hipError_t launch_skinny_long(const uint16_t *x, const int8_t *Q, const f
   }
 }
 
+// Batched GEMV for up to 16 MB x rows (MB groups of 16; used for 33-48 rows)
+// at K = 1024 j <= 4096:
+// the long-K skinny kernel's step structure with passes of 1 KB of every row,
+// so that the eight waves' shares of a pass (128 bytes of a row each) leave
+// room in registers for the x fragments of all MB groups, in two sets (the
+// next pass's loads are issued just before its first weight loads, as there).
+// A step is one (pass, 16-row tile): each wave loads its 128-byte share of
+// the tile's rows into registers, writes them to its own LDS region through
+// the chunk swizzle, and multiplies the widened fragments against every x
+// group's fragments (one accumulator chain per group and tile).  The waves'
+// partial tiles are added in K order through LDS at the end.
+template <int NP, int TILES, int MB>
+__global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
+    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q,
+    const float *__restrict__ scales, const float *__restrict__ bias, int epi,
+    uint16_t *__restrict__ y, int M, int N, int K) {
+  constexpr int NWV = 8;
+  constexpr int KQ = 1024 / NWV;  // bytes of a row per wave per pass
+  constexpr int NJ = KQ / 64;     // 64-deep blocks per wave per pass
+  constexpr int CP = KQ / 64;     // 1-KB loads per wave per step (16 KQ bytes)
+  constexpr int SLOT = 16 * KQ;
+  constexpr int STEPS = NP * TILES;
+  constexpr int XL = 2 * MB * NJ;  // x loads per pass
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, c = lane >> 4;
+  const int n0 = blockIdx.x * 16 * TILES;
+  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
+  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
+  uint8_t *mine = lds8 + wave * 2 * SLOT;
+
+  uint4 xa[2][MB][NJ], xb[2][MB][NJ];
+  // x fragments of pass p into set p & 1: group g, block j: x row 16 g + r,
+  // k = 1024 p + KQ wave + 64 j + 16 c .. + 15 (zero past M)
+  auto load_x = [&](int p) {
+#pragma unroll
+    for (int g = 0; g < MB; ++g)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int row = 16 * g + r;
+        const int k = 1024 * p + wave * KQ + 64 * j + 16 * c;
+        const uint32_t xo = row < M ? (uint32_t)((row * K + k) * 2) : kOobOffset;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        const u32x4 b =
+            __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
+        xa[p & 1][g][j] = make_uint4(a[0], a[1], a[2], a[3]);
+        xb[p & 1][g][j] = make_uint4(b[0], b[1], b[2], b[3]);
+      }
+  };
+  uint4 R[2][CP];
+  // step st = (pass p, tile t): load i, lane l holds LDS byte e = 1024 i + 16 l
+  // of the wave's region, row e / KQ, chunk (e % KQ) / 16 from global chunk
+  // chunk ^ (row & 7)
+  auto issue = [&](int st) {
+    const int p = st / TILES, t = st % TILES;
+#pragma unroll
+    for (int i = 0; i < CP; ++i) {
+      const int e = 1024 * i + 16 * lane;
+      const int rr = e / KQ, ch = (e - rr * KQ) >> 4;
+      const uint32_t off =
+          (uint32_t)((t * 16 + rr) * K + 1024 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rQ, off, 0, 2 /* nt */);
+      R[st & 1][i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  load_x(0);
+  issue(0);
+  if (STEPS > 1) {
+    if (TILES == 1) load_x(1);
+    issue(1);
+  }
+  f32x4 acc[TILES][MB];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int g = 0; g < MB; ++g) acc[t][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int p = st / TILES, t = st % TILES;
+    // step st landed (and its pass's x): at most step st + 1's loads, and the
+    // x loads of the pass it opens, still outstanding
+    if (st + 1 < STEPS) {
+      if ((st + 1) % TILES == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP + XL));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < CP; ++i)
+      *(uint4 *)(mine + (st & 1) * SLOT + 1024 * i + 16 * lane) = R[st & 1][i];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+    const uint8_t *src = mine + (st & 1) * SLOT + r * KQ;
+    uint4 qv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) qv[j] = *(const uint4 *)(src + 16 * ((4 * j + c) ^ (r & 7)));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
+      const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
+#pragma unroll
+      for (int g = 0; g < MB; ++g) {
+        acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w0, __builtin_bit_cast(bf16x8, xa[p & 1][g][j]), acc[t][g], 0, 0, 0);
+        acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            w1, __builtin_bit_cast(bf16x8, xb[p & 1][g][j]), acc[t][g], 0, 0, 0);
+      }
+    }
+    if (st + 2 < STEPS) {
+      // this wave's fragment reads of the region are done before it is refilled
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+      if ((st + 2) % TILES == 0) load_x((st + 2) / TILES);
+      issue(st + 2);
+    }
+  }
+  __syncthreads();
+  f32x4 *red = (f32x4 *)lds8;
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int g = 0; g < MB; ++g) red[((wave * TILES + t) * MB + g) * 64 + lane] = acc[t][g];
+  __syncthreads();
+  if (wave >= TILES) return;
+#pragma unroll
+  for (int g = 0; g < MB; ++g) {
+    f32x4 sum = red[((0 * TILES + wave) * MB + g) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + wave) * MB + g) * 64 + lane];
+    const int m = 16 * g + r;
+    if (m >= M) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + 16 * wave + 4 * c + q;
+      if (n >= N) break;
+      float v;
+      {
+#pragma clang fp contract(off)
+        v = sum[q] * scales[n];
+        if (bias) v = v + bias[n];
+      }
+      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+    }
+  }
+}
+
+template <int NP, int TILES, int MB>
+static hipError_t launch_mid_k(const uint16_t *x, const int8_t *Q, const float *scales,
+                               const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
+                               int64_t K, hipStream_t stream) {
+  constexpr size_t slots = size_t(8) * 2 * 16 * 128;
+  constexpr size_t red = size_t(8) * TILES * MB * 64 * sizeof(f32x4);
+  constexpr size_t lds = slots > red ? slots : red;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  auto kern = gemv_w8a16_mid_kernel<NP, TILES, MB>;
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit, std::memory_order_release);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))), dim3(512), lds,
+                     stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+  return hipGetLastError();
+}
+
+// K = 1024 NP (NP <= 4), up to 16 MB x rows
+template <int TILES, int MB>
+static hipError_t launch_mid(const uint16_t *x, const int8_t *Q, const float *scales,
+                             const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
+                             int64_t K, hipStream_t stream) {
+  switch (K / 1024) {
+    case 1: return launch_mid_k<1, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    case 2: return launch_mid_k<2, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    case 3: return launch_mid_k<3, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    case 4: return launch_mid_k<4, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // Decode GEMV for one x row (M = 1, K = 1024, 2048, 3072 or 4096): persistent
 // streaming.
 //
@@ -1439,6 +1626,11 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
     // kernel; 4096 x 11008: 10.1 against 14.4 on the long-K MFMA GEMV
     return launch_ksplit_m_k<2, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K,
                                        stream);
+  if (M > 32 && M <= 48 && K % 1024 == 0 && K <= 4096)
+    // 11008 x 4096 at M = 33 / 48 / 64: 20.5-20.9 / 22.6-22.7 / 26.1 us against
+    // 25.4 / 25.7 / 26.3 on the W8A16 tile GEMM (the x reads, M K 2 bytes per
+    // workgroup, grow with M); 32 or 16 weight rows per workgroup: 31.6-59.7 us
+    return launch_mid<3, 4>(x, Q, scales, bias, epi, y, M, N, K, stream);
   if (M >= kGemvMfmaMinM && M <= 32 && K % 1024 == 0 && K <= 4096) {
     if (M <= 16)
       return launch_skinny<3, 8, 1>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);

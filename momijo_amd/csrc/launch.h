@@ -108,9 +108,10 @@ hipError_t launch_cast_i64_f32(const int64_t *x, float *y, int64_t n, hipStream_
 // 11008 x 4096 where the 256-row GEMM tile takes 38 us).
 constexpr int64_t kGemvMaxM = 16;
 // Whether launch_gemv_w8a16 takes an M-row W8A16 product: every M <= 16, and
-// 17..32 rows when K = 1024 j <= 4096 (the skinny kernel's two x-row groups).
+// 17..48 rows when K = 1024 j <= 4096 (the skinny kernel's two x-row groups up
+// to 32 rows, the batched GEMV's four beyond).
 inline bool gemv_w8a16_takes(int64_t M, int64_t K) {
-  return M <= kGemvMaxM || (M <= 32 && K % 1024 == 0 && K > 0 && K <= 4096);
+  return M <= kGemvMaxM || (M <= 48 && K % 1024 == 0 && K > 0 && K <= 4096);
 }
 hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *scales,
                              const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,

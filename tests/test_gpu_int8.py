@@ -284,7 +284,7 @@ def test_c3_gemv(oracle, dev):
     assert err <= BF16_TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16, 17, 32])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16, 17, 32, 33, 48])
 @pytest.mark.parametrize("N,K", [(64, 256), (37, 1040), (300, 4096), (5, 16), (17, 48),
                                  (130, 11008), (48, 6160)])
 def test_gemv_shapes(oracle, dev, M, N, K):
@@ -383,7 +383,12 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    # skinny MFMA GEMV, 2-4 passes (the last one
                                    # 1-4 KB and past K), partial tiles
                                    (5, 300, 5008), (9, 37, 12304), (16, 4100, 8192),
-                                   (16, 1000, 16384)])
+                                   (16, 1000, 16384),
+                                   # 33-48 x rows at K = 1024 j: the batched
+                                   # GEMV's four x-row groups over 1-KB passes
+                                   # (64: the tile GEMM again)
+                                   (33, 300, 1024), (40, 37, 2048), (48, 4100, 4096),
+                                   (48, 11008, 4096), (64, 1000, 3072)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
