@@ -278,471 +278,48 @@ __global__ __launch_bounds__(KQ * 64) void gemv_w8a16_mfma_kernel(const uint16_t
   }
 }
 
-// Skinny-M W8A16 GEMV for 3 <= M <= 32 (MB groups of 16 x rows) and K = 1024 j
-// (j <= 4), plain or the FFN's gate/up (GATEUP: the workgroup's tiles alternate
-// 16 gate rows and the 16 up rows of the same output columns, and the epilogue
-// forms bf16(silu(g sg) (u su)) from the two fp32 tile sums): the weights
-// stream as whole row pieces and reach the MFMA through LDS.  NWV waves split
-// K (KQ = K / NWV bytes of every row each); a workgroup owns 16 TILES weight
-// rows.  For each 16-row tile a wave copies its share of the 16 rows into its
-// own LDS region, 1 KB per instruction (1024 / KQ rows of KQ contiguous bytes):
-// with REG through registers (buffer loads, then ds_write once they landed),
-// else straight (buffer_load ... lds); two tiles in flight.  It then reads the MFMA
-// fragments from there: lane (r, c) takes 16 int8 of row r at 16-byte chunk
-// 4 j + c of 64-deep block j, widened exactly to bf16, the first 8 k for one
-// v_mfma_f32_16x16x32_bf16 and the other 8 for the second, against x
-// fragments of the same k that the wave loaded once, into registers, at the
-// start.  Chunk p of row r is stored at LDS chunk p ^ (r & 7), so the 8 lanes
-// of a 128-byte read phase hit distinct banks.  No barrier in the loop: a wave
-// reads only its own region.  The NWV partial 16 x 16 tiles of a row tile are
-// added in K order through LDS (deterministic), then scale, bias and the
-// activation.
-// Measured on MI355X at 11008 x 4096 (graph replay over 8 weight copies):
-// M = 3, 8, 16 13.3, 13.7, 15.1 us against 15.3, 17.3, 19.4 for
-// gemv_w8a16_mfma_kernel (16 weight rows per workgroup, x re-read per 16 rows,
-// 64 bytes of a row per load instruction); four waves of 1-KB rows 13.5, 14.1,
-// 15.6.  The copies alone (no fragment reads, no MFMA) take 9.2 us with four
-// waves, 10.8 with eight; the rest is the widening (1.5 VALU per weight).
-// Refilling a slot as soon as its fragments are in registers (two tiles in
-// flight during the compute) measured slower, and a third slot does not fit
-// the LDS.  Through registers (REG) the same launches take 12.2, 12.3, 13.8
-// us at M = 3, 8, 16 (alternating runs on one box: 13.4, 13.6, 15.4 straight
-// into LDS); with two x groups (232-248 VGPRs) they take 1 us longer, so M
-// > 16 copies straight.
-__device__ __forceinline__ void dma16_lds(__amdgpu_buffer_rsrc_t r, void *lds_dst, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, (__attribute__((address_space(3))) void *)lds_dst, 16, off, 0, 0, 2 /* nt */);
-}
-
 // s_waitcnt immediate: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F70; }
 
-template <int TILES, int KB, int NWV, int MB, bool GATEUP, bool REG = false>
-__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_kernel(
+// Skinny-M W8A16 GEMV for 3..48 x rows (MB groups of 16), plain or the FFN's
+// gate/up (GATEUP: the workgroup's tiles alternate 16 gate rows and the 16 up
+// rows of the same output columns; the epilogue forms bf16(silu(g sg) (u su))
+// from the two fp32 tile sums).  With several x rows the streaming GEMV's
+// per-lane multiply-adds turn VALU-bound, so the products go to
+// v_mfma_f32_16x16x32_bf16 and the lanes only widen the weights (int8 ->
+// bf16, exact).  K is taken in NP passes of 1 KB of every row; a step is one
+// (pass, 16-row tile), passes outermost, TILES tiles per workgroup.  Eight
+// waves split each pass (128 bytes of a row each): per step a wave loads its
+// share of the tile's 16 rows into registers (two 1-KB loads of 8 rows x 128
+// contiguous bytes), writes them to its own LDS region with chunk p of row r
+// at chunk p ^ (r & 7) (the 8 lanes of a 128-byte read phase then hit
+// distinct banks) and reads the MFMA fragments back: lane (r, c) takes the 16
+// int8 of row r at chunk 4 j + c of 64-deep block j, the first 8 k for one
+// MFMA and the other 8 for the second, against x fragments of the same k.
+// The x fragments of all MB groups for a pass sit in registers, in two sets:
+// the next pass's loads are issued just before its first weight loads (one
+// wait then covers both: loads retire in order) while the current pass still
+// reads the other set.  Two steps in flight; no barrier in the loop (a wave
+// reads only its own region).  Past K (K rounded up to 1 KB) the x fragments
+// load zero and the weight bytes there (the next row's, or zero past the
+// buffer) add exact zeros.  The eight waves' partial tiles are added in K
+// order through LDS (deterministic), then scale, bias and the activation.
+// Measured on MI355X, 11008 x 4096 weights (graph replay over 8 weight copies,
+// alternating runs on one box): M = 3 / 8 / 16 / 17 / 32 10.9-11.1 / 10.8 /
+// 12.0 / 13.9 / 16.7 us against 12.0-12.2 / 12.3 / 13.7 / 16.3 / 19.2 for the
+// same design with one 4-KB pass (the fill and drain of its three steps were
+// a third of a workgroup's life) and 13.3 / 13.7 / 15.1 / 17.6 / 20.5 with the
+// weights copied straight into LDS (buffer_load ... lds); M = 33 / 48 / 64
+// 20.5-20.9 / 22.6 / 26.1 against 25.4 / 25.7 / 26.3 on the W8A16 tile GEMM
+// (every workgroup reads all of x, M K 2 bytes, which sets the time as M
+// grows).  The FFN's down projection (4096 x 11008, one tile per workgroup) at
+// M = 5 / 8 / 16: 13.1-13.2 / 13.7-13.8 / 16.7 us against 14.0 / 14.5 / 18.2
+// with 4-KB passes.
+template <int NP, int TILES, int MB, bool GATEUP>
+__global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
     const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
     const float *__restrict__ scales, const float *__restrict__ scales2,
     const float *__restrict__ bias, int epi, uint16_t *__restrict__ y, int M, int N, int K) {
-  constexpr int TP = GATEUP ? TILES / 2 : TILES;  // 16-column output tiles
-  static_assert(!GATEUP || TILES % 2 == 0, "gate/up tiles come in pairs");
-  constexpr int NJ = 64 / NWV;         // most 64-deep blocks per wave (K <= 4096)
-  constexpr int SLOT = 65536 / NWV;    // bytes of one tile's share at K = 4096
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane & 15, c = lane >> 4;
-  const int n0 = blockIdx.x * 16 * TP;
-  const int rows = N - n0 < 16 * TP ? N - n0 : 16 * TP;
-  constexpr int KQ = 512 * KB / NWV;  // bytes of a row per wave (K = 512 KB)
-  static_assert(KQ >= 128, "eight 16-byte chunks per row share");
-  constexpr int nj = KQ / 64;    // 64-deep blocks per wave
-  constexpr int ninst = KQ / 64; // 1-KB copies per tile (16 KQ bytes)
-  const int kq0 = wave * KQ;
-  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
-  const __amdgpu_buffer_rsrc_t rQ2 =
-      make_rsrc((GATEUP ? Q2 : Q) + (size_t)n0 * K, (int64_t)rows * K);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
-  uint8_t *mine = lds8 + wave * 2 * SLOT;
-
-  // x fragments of this wave's share, once: group g holds x rows 16 g + r
-  uint4 xa[MB][NJ], xb[MB][NJ];
-#pragma unroll
-  for (int g = 0; g < MB; ++g)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      xa[g][j] = xb[g][j] = make_uint4(0, 0, 0, 0);
-      if (j < nj) {
-        const uint32_t xo = 16 * g + r < M
-                                ? (uint32_t)(((16 * g + r) * K + kq0 + 64 * j + 16 * c) * 2)
-                                : kOobOffset;
-        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-        const u32x4 b =
-            __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
-        xa[g][j] = make_uint4(a[0], a[1], a[2], a[3]);
-        xb[g][j] = make_uint4(b[0], b[1], b[2], b[3]);
-      }
-    }
-  // tile t's share -> slot t & 1: copy i, lane l fills LDS byte e = 1024 i + 16 l
-  // of the slot, row e / KQ, chunk p = (e % KQ) / 16, from global chunk p ^ (row & 7).
-  // GATEUP: tile 2 j is gate rows 16 j.., tile 2 j + 1 the up rows of the same columns
-  // tiles in flight (three, with registers for them, measured 0.6-0.8 us slower
-  // at 3-16 x rows)
-  constexpr int DEPTH = 2;
-  uint4 R[DEPTH][REG ? ninst : 1];
-  auto issue = [&](int t) {
-    uint8_t *dst = mine + (t & 1) * SLOT;
-    const int tr = GATEUP ? t >> 1 : t;
-#pragma unroll
-    for (int i = 0; i < ninst; ++i) {
-      const int e = 1024 * i + 16 * lane;
-      const int rr = e / KQ, p = (e - rr * KQ) >> 4;
-      const uint32_t off = (uint32_t)((tr * 16 + rr) * K + kq0 + 16 * (p ^ (rr & 7)));
-      if constexpr (REG) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (t & 1)) ? rQ2 : rQ,
-                                                              off, 0, 2 /* nt */);
-        R[t % DEPTH][i] = make_uint4(v[0], v[1], v[2], v[3]);
-      } else {
-        dma16_lds((GATEUP && (t & 1)) ? rQ2 : rQ, dst + 1024 * i, off);
-      }
-    }
-  };
-#pragma unroll
-  for (int t = 0; t < DEPTH; ++t)
-    if (t < TILES) issue(t);
-  f32x4 acc[TILES][MB];
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) {
-    // tile t landed: at most the loads of the next DEPTH - 1 tiles outstanding
-    const int later = TILES - 1 - t < DEPTH - 1 ? TILES - 1 - t : DEPTH - 1;
-    if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * ninst));
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(ninst));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    asm volatile("" ::: "memory");
-    if constexpr (REG) {
-#pragma unroll
-      for (int i = 0; i < ninst; ++i)
-        *(uint4 *)(mine + (t & 1) * SLOT + 1024 * i + 16 * lane) = R[t % DEPTH][i];
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("" ::: "memory");
-    }
-    const uint8_t *src = mine + (t & 1) * SLOT + r * KQ;
-    // two independent accumulator chains per x group (the chunk halves), added
-    // in a fixed order at the end
-    f32x4 ch[MB][2];
-#pragma unroll
-    for (int g = 0; g < MB; ++g) ch[g][0] = ch[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 qv[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (j < nj) qv[j] = *(const uint4 *)(src + 16 * ((4 * j + c) ^ (r & 7)));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      if (j < nj) {
-        const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
-        const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
-#pragma unroll
-        for (int g = 0; g < MB; ++g) {
-          ch[g][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              w0, __builtin_bit_cast(bf16x8, xa[g][j]), ch[g][0], 0, 0, 0);
-          ch[g][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              w1, __builtin_bit_cast(bf16x8, xb[g][j]), ch[g][1], 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < MB; ++g) acc[t][g] = ch[g][0] + ch[g][1];
-    if (t + DEPTH < TILES) {
-      // this wave's fragment reads of the slot are done before it is refilled
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("" ::: "memory");
-      issue(t + DEPTH);
-    }
-  }
-  // every wave is past its last fragment read (and its copies have landed):
-  // the slots become the partials [NWV][TILES][MB][64]
-  __syncthreads();
-  f32x4 *red = (f32x4 *)lds8;
-#pragma unroll
-  for (int t = 0; t < TILES; ++t)
-#pragma unroll
-    for (int g = 0; g < MB; ++g) red[((wave * TILES + t) * MB + g) * 64 + lane] = acc[t][g];
-  __syncthreads();
-  if (wave >= TP) return;
-  // wave w: output columns n0 + 16 w.. (tile w, or gate tile 2 w and up tile 2 w + 1)
-  constexpr int TS = GATEUP ? 2 : 1;
-#pragma unroll
-  for (int g = 0; g < MB; ++g) {
-    f32x4 sum = red[((0 * TILES + TS * wave) * MB + g) * 64 + lane];
-#pragma unroll
-    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + TS * wave) * MB + g) * 64 + lane];
-    f32x4 sum2 = sum;
-    if constexpr (GATEUP) {
-      sum2 = red[((0 * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
-#pragma unroll
-      for (int w = 1; w < NWV; ++w) sum2 += red[((w * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
-    }
-    // lane: x row m = 16 g + lane % 16, output columns n0 + 16 wave + 4 (lane / 16) + q
-    const int m = 16 * g + r;
-    if (m >= M) continue;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = n0 + 16 * wave + 4 * c + q;
-      if (n >= N) break;
-      float v;
-      if constexpr (GATEUP) {
-        const float gv = epi_scale_bias(sum[q], scales[n], 0.0f, true, false);
-        const float uv = epi_scale_bias(sum2[q], scales2[n], 0.0f, true, false);
-        {
-#pragma clang fp contract(off)
-          v = silu_b16(gv) * uv;
-        }
-      } else {
-        {
-#pragma clang fp contract(off)
-          v = sum[q] * scales[n];
-          if (bias) v = v + bias[n];
-        }
-        v = apply_epi_b16(epi, v);
-      }
-      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
-    }
-  }
-}
-
-template <int TILES, int KB, int NWV, int MB, bool GATEUP, bool REG>
-static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
-                                  const float *scales, const float *scales2, const float *bias,
-                                  int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
-                                  hipStream_t stream) {
-  constexpr size_t lds = 2 * 65536;
-  static_assert(NWV * TILES * MB * 64 * sizeof(f32x4) <= lds, "partials fit the slots");
-  auto kern = gemv_w8a16_skinny_kernel<TILES, KB, NWV, MB, GATEUP, REG>;
-  static std::atomic<uint64_t> attr_set{0};
-  int dev = 0;
-  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set.fetch_or(bit, std::memory_order_release);
-  }
-  constexpr int cols = 16 * (GATEUP ? TILES / 2 : TILES);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + cols - 1) / cols)), dim3(NWV * 64), lds, stream,
-                     x, Q, Q2, scales, scales2, bias, epi, y, (int)M, (int)N, (int)K);
-  return hipGetLastError();
-}
-
-template <int TILES, int NWV, int MB, bool GATEUP = false>
-static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
-                                const float *scales, const float *scales2, const float *bias,
-                                int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
-                                hipStream_t stream) {
-  // one x group: the weights through registers; two (232-248 VGPRs): straight
-  // into LDS (the register path measured 1 us slower there)
-  constexpr bool REG = MB == 1;
-  switch (K / 512) {
-#define MJ_SK(kb)                                                                             \
-  case kb:                                                                                    \
-    return launch_skinny_k<TILES, kb, NWV, MB, GATEUP, REG>(x, Q, Q2, scales, scales2, bias,  \
-                                                            epi, y, M, N, K, stream);
-    MJ_SK(2) MJ_SK(4) MJ_SK(6) MJ_SK(8)
-#undef MJ_SK
-    default: return hipErrorInvalidValue;
-  }
-}
-
-// The skinny GEMV at K > 4096 (the FFN's down projection at K = 11008), up to
-// 16 x rows.  K is taken in NP passes: NP - 1 of 4096 bytes of every row and a
-// last one of 512 KBL bytes that covers the rest (K rounded up to 1024).  A
-// step is one (pass, tile) pair, passes outermost: each wave copies its
-// 4096 / NWV-byte (last pass 64 KBL) share of the tile's 16 rows into its own
-// LDS slot through registers as the K <= 4096 kernel does with REG (two steps
-// in flight; 1.0-1.3 us faster at M = 5-16 than copies straight into LDS), and
-// multiplies it against the x fragments of that pass, which sit in one of two
-// register sets: the next pass's x loads are issued just before its first
-// copy, so the wait for that copy also covers them, while the current pass
-// still reads the other set.  Where a pass runs past K the x fragments are
-// zero (their loads are out of range) and the weight bytes there (the next
-// row's first bytes, or zero past the buffer) add exact zeros.  The tile
-// sums build up over the passes in registers; the waves' partials are added
-// in K order through LDS at the end, as above.
-template <int NP, int KBL, int TILES, int NWV>
-__global__ __launch_bounds__(NWV * 64) void gemv_w8a16_skinny_long_kernel(
-    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q,
-    const float *__restrict__ scales, const float *__restrict__ bias, int epi,
-    uint16_t *__restrict__ y, int M, int N, int K) {
-  constexpr int SLOT = 65536 / NWV;  // a full pass's share of one tile
-  constexpr int KQF = 4096 / NWV;    // bytes of a row per wave, full pass
-  constexpr int KQL = 512 * KBL / NWV;
-  static_assert(KQL >= 128 && KQL <= KQF, "eight 16-byte chunks per row share");
-  constexpr int NJ = KQF / 64;
-  constexpr int STEPS = NP * TILES;
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane & 15, c = lane >> 4;
-  const int n0 = blockIdx.x * 16 * TILES;
-  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
-  const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
-  uint8_t *mine = lds8 + wave * 2 * SLOT;
-
-  uint4 xa[2][NJ], xb[2][NJ];
-  // x fragments of pass p into set p & 1: lane (r, c) block j holds x row r,
-  // k = 4096 p + KQ wave + 64 j + 16 c .. + 15 (zero at k >= K or r >= M;
-  // K % 16 == 0 keeps a fragment all in or all out)
-  auto load_x = [&](int p) {
-    const int KQ = p + 1 < NP ? KQF : KQL;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      if (j < KQ / 64) {
-        const int k = 4096 * p + wave * KQ + 64 * j + 16 * c;
-        const uint32_t xo = r < M && k < K ? (uint32_t)((r * K + k) * 2) : kOobOffset;
-        const uint32_t xo2 = xo == kOobOffset ? xo : xo + 16;
-        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, xo2, 0, 0);
-        xa[p & 1][j] = make_uint4(a[0], a[1], a[2], a[3]);
-        xb[p & 1][j] = make_uint4(b[0], b[1], b[2], b[3]);
-      }
-    }
-  };
-  // vector memory instructions of one step's copies and of one pass's x loads
-  constexpr int kCopiesF = KQF / 64, kCopiesL = KQL / 64;
-  constexpr int kXLoadsF = 2 * kCopiesF, kXLoadsL = 2 * kCopiesL;
-  // step st = (pass p, tile t) -> slot st & 1, as the K <= 4096 kernel's copies
-  uint4 R[2][KQF / 64];
-  auto issue = [&](int st) {
-    const int p = st / TILES, t = st % TILES;
-    const int KQ = p + 1 < NP ? KQF : KQL;
-#pragma unroll
-    for (int i = 0; i < KQF / 64; ++i) {
-      if (i < KQ / 64) {
-        const int e = 1024 * i + 16 * lane;
-        const int rr = e / KQ, ch = (e - rr * KQ) >> 4;
-        const uint32_t off =
-            (uint32_t)((t * 16 + rr) * K + 4096 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rQ, off, 0, 2 /* nt */);
-        R[st & 1][i] = make_uint4(v[0], v[1], v[2], v[3]);
-      }
-    }
-  };
-  load_x(0);
-  issue(0);
-  if (STEPS > 1) {
-    if (TILES == 1) load_x(1);
-    issue(1);
-  }
-  f32x4 acc[TILES];
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int st = 0; st < STEPS; ++st) {
-    const int p = st / TILES, t = st % TILES;
-    const int KQ = p + 1 < NP ? KQF : KQL;
-    // step st landed (and its pass's x): at most step st + 1's copies, and the
-    // x loads of the pass it opens, still outstanding
-    if (st + 1 < STEPS) {
-      const bool opens = (st + 1) % TILES == 0, last = (st + 1) / TILES + 1 == NP;
-      if (opens && last) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesL + kXLoadsL));
-      else if (opens) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesF + kXLoadsF));
-      else if (last) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesL));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopiesF));
-    } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    }
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < KQF / 64; ++i)
-      if (i < KQ / 64) *(uint4 *)(mine + (st & 1) * SLOT + 1024 * i + 16 * lane) = R[st & 1][i];
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    asm volatile("" ::: "memory");
-    const uint8_t *src = mine + (st & 1) * SLOT + r * KQ;
-    f32x4 ch0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, ch1 = ch0;
-    uint4 qv[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (j < KQ / 64) qv[j] = *(const uint4 *)(src + 16 * ((4 * j + c) ^ (r & 7)));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      if (j < KQ / 64) {
-        const bf16x8 w0 = i8x8_bf16(qv[j].x, qv[j].y);
-        const bf16x8 w1 = i8x8_bf16(qv[j].z, qv[j].w);
-        ch0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w0, __builtin_bit_cast(bf16x8, xa[p & 1][j]), ch0, 0, 0, 0);
-        ch1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w1, __builtin_bit_cast(bf16x8, xb[p & 1][j]), ch1, 0, 0, 0);
-      }
-    }
-    acc[t] += ch0 + ch1;
-    if (st + 2 < STEPS) {
-      // this wave's fragment reads of the slot are done before it is refilled
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("" ::: "memory");
-      if ((st + 2) % TILES == 0) load_x((st + 2) / TILES);
-      issue(st + 2);
-    }
-  }
-  __syncthreads();
-  f32x4 *red = (f32x4 *)lds8;
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) red[(wave * TILES + t) * 64 + lane] = acc[t];
-  __syncthreads();
-  if (wave >= TILES) return;
-  f32x4 sum = red[wave * 64 + lane];
-#pragma unroll
-  for (int w = 1; w < NWV; ++w) sum += red[(w * TILES + wave) * 64 + lane];
-  if (r >= M) return;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int n = n0 + 16 * wave + 4 * c + q;
-    if (n >= N) break;
-    float v;
-    {
-#pragma clang fp contract(off)
-      v = sum[q] * scales[n];
-      if (bias) v = v + bias[n];
-    }
-    y[(size_t)r * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
-  }
-}
-
-template <int NP, int KBL, int TILES>
-static hipError_t launch_skinny_long_k(const uint16_t *x, const int8_t *Q, const float *scales,
-                                       const float *bias, int epi, uint16_t *y, int64_t M,
-                                       int64_t N, int64_t K, hipStream_t stream) {
-  constexpr int NWV = 8;
-  constexpr size_t lds = 2 * 65536;
-  auto kern = gemv_w8a16_skinny_long_kernel<NP, KBL, TILES, NWV>;
-  static std::atomic<uint64_t> attr_set{0};
-  int dev = 0;
-  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set.fetch_or(bit, std::memory_order_release);
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))),
-                     dim3(NWV * 64), lds, stream, x, Q, scales, bias, epi, y, (int)M, (int)N,
-                     (int)K);
-  return hipGetLastError();
-}
-
-// K = 4096 (NP - 1) + 512 KBL after rounding K up to 1024 (4096 < K <= 16384)
-template <int TILES>
-static hipError_t launch_skinny_long(const uint16_t *x, const int8_t *Q, const float *scales,
-                                     const float *bias, int epi, uint16_t *y, int64_t M,
-                                     int64_t N, int64_t K, hipStream_t stream) {
-  const int64_t kp = (K + 1023) / 1024;  // 1-KB units
-  const int np = (int)((kp + 3) / 4), kbl = (int)(2 * (kp - 4 * (np - 1)));
-  switch (np * 10 + kbl) {
-#define MJ_SL(np_, kbl_)                                                                      \
-  case np_ * 10 + kbl_:                                                                       \
-    return launch_skinny_long_k<np_, kbl_, TILES>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    MJ_SL(2, 2) MJ_SL(2, 4) MJ_SL(2, 6) MJ_SL(2, 8) MJ_SL(3, 2) MJ_SL(3, 4) MJ_SL(3, 6)
-    MJ_SL(3, 8) MJ_SL(4, 2) MJ_SL(4, 4) MJ_SL(4, 6) MJ_SL(4, 8)
-#undef MJ_SL
-    default: return hipErrorInvalidValue;
-  }
-}
-
-// Batched GEMV for up to 16 MB x rows (MB groups of 16; used for 33-48 rows)
-// at K = 1024 j <= 4096:
-// the long-K skinny kernel's step structure with passes of 1 KB of every row,
-// so that the eight waves' shares of a pass (128 bytes of a row each) leave
-// room in registers for the x fragments of all MB groups, in two sets (the
-// next pass's loads are issued just before its first weight loads, as there).
-// A step is one (pass, 16-row tile): each wave loads its 128-byte share of
-// the tile's rows into registers, writes them to its own LDS region through
-// the chunk swizzle, and multiplies the widened fragments against every x
-// group's fragments (one accumulator chain per group and tile).  The waves'
-// partial tiles are added in K order through LDS at the end.
-template <int NP, int TILES, int MB>
-__global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
-    const uint16_t *__restrict__ x, const int8_t *__restrict__ Q,
-    const float *__restrict__ scales, const float *__restrict__ bias, int epi,
-    uint16_t *__restrict__ y, int M, int N, int K) {
   constexpr int NWV = 8;
   constexpr int KQ = 1024 / NWV;  // bytes of a row per wave per pass
   constexpr int NJ = KQ / 64;     // 64-deep blocks per wave per pass
@@ -750,19 +327,25 @@ __global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
   constexpr int SLOT = 16 * KQ;
   constexpr int STEPS = NP * TILES;
   constexpr int XL = 2 * MB * NJ;  // x loads per pass
+  constexpr int TP = GATEUP ? TILES / 2 : TILES;  // 16-column output tiles
+  static_assert(!GATEUP || TILES % 2 == 0, "gate/up tiles come in pairs");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
-  const int n0 = blockIdx.x * 16 * TILES;
-  const int rows = N - n0 < 16 * TILES ? N - n0 : 16 * TILES;
+  const int n0 = blockIdx.x * 16 * TP;
+  const int rows = N - n0 < 16 * TP ? N - n0 : 16 * TP;
   const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q + (size_t)n0 * K, (int64_t)rows * K);
+  const __amdgpu_buffer_rsrc_t rQ2 =
+      make_rsrc((GATEUP ? Q2 : Q) + (size_t)n0 * K, (int64_t)rows * K);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
   uint8_t *mine = lds8 + wave * 2 * SLOT;
 
   uint4 xa[2][MB][NJ], xb[2][MB][NJ];
   // x fragments of pass p into set p & 1: group g, block j: x row 16 g + r,
-  // k = 1024 p + KQ wave + 64 j + 16 c .. + 15 (zero past M)
+  // k = 1024 p + KQ wave + 64 j + 16 c .. + 15 (zero past M or K; K % 16 == 0
+  // keeps a fragment all in or all out).  Past K the weight bytes (the next
+  // row's, or zero past the buffer) then add exact zeros.
   auto load_x = [&](int p) {
 #pragma unroll
     for (int g = 0; g < MB; ++g)
@@ -770,7 +353,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
       for (int j = 0; j < NJ; ++j) {
         const int row = 16 * g + r;
         const int k = 1024 * p + wave * KQ + 64 * j + 16 * c;
-        const uint32_t xo = row < M ? (uint32_t)((row * K + k) * 2) : kOobOffset;
+        const uint32_t xo = row < M && k < K ? (uint32_t)((row * K + k) * 2) : kOobOffset;
         const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
         const u32x4 b =
             __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
@@ -781,16 +364,19 @@ __global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
   uint4 R[2][CP];
   // step st = (pass p, tile t): load i, lane l holds LDS byte e = 1024 i + 16 l
   // of the wave's region, row e / KQ, chunk (e % KQ) / 16 from global chunk
-  // chunk ^ (row & 7)
+  // chunk ^ (row & 7).  GATEUP: tile 2 j is gate rows 16 j.., tile 2 j + 1
+  // the up rows of the same columns.
   auto issue = [&](int st) {
     const int p = st / TILES, t = st % TILES;
+    const int tr = GATEUP ? t >> 1 : t;
 #pragma unroll
     for (int i = 0; i < CP; ++i) {
       const int e = 1024 * i + 16 * lane;
       const int rr = e / KQ, ch = (e - rr * KQ) >> 4;
       const uint32_t off =
-          (uint32_t)((t * 16 + rr) * K + 1024 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rQ, off, 0, 2 /* nt */);
+          (uint32_t)((tr * 16 + rr) * K + 1024 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (t & 1)) ? rQ2 : rQ,
+                                                            off, 0, 2 /* nt */);
       R[st & 1][i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
   };
@@ -853,12 +439,20 @@ __global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
 #pragma unroll
     for (int g = 0; g < MB; ++g) red[((wave * TILES + t) * MB + g) * 64 + lane] = acc[t][g];
   __syncthreads();
-  if (wave >= TILES) return;
+  if (wave >= TP) return;
+  // wave w: output columns n0 + 16 w.. (tile w, or gate tile 2 w and up tile 2 w + 1)
+  constexpr int TS = GATEUP ? 2 : 1;
 #pragma unroll
   for (int g = 0; g < MB; ++g) {
-    f32x4 sum = red[((0 * TILES + wave) * MB + g) * 64 + lane];
+    f32x4 sum = red[((0 * TILES + TS * wave) * MB + g) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + wave) * MB + g) * 64 + lane];
+    for (int w = 1; w < NWV; ++w) sum += red[((w * TILES + TS * wave) * MB + g) * 64 + lane];
+    f32x4 sum2 = sum;
+    if constexpr (GATEUP) {
+      sum2 = red[((0 * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) sum2 += red[((w * TILES + 2 * wave + 1) * MB + g) * 64 + lane];
+    }
     const int m = 16 * g + r;
     if (m >= M) continue;
 #pragma unroll
@@ -866,25 +460,36 @@ __global__ __launch_bounds__(512) void gemv_w8a16_mid_kernel(
       const int n = n0 + 16 * wave + 4 * c + q;
       if (n >= N) break;
       float v;
-      {
+      if constexpr (GATEUP) {
+        const float gv = epi_scale_bias(sum[q], scales[n], 0.0f, true, false);
+        const float uv = epi_scale_bias(sum2[q], scales2[n], 0.0f, true, false);
+        {
 #pragma clang fp contract(off)
-        v = sum[q] * scales[n];
-        if (bias) v = v + bias[n];
+          v = silu_b16(gv) * uv;
+        }
+      } else {
+        {
+#pragma clang fp contract(off)
+          v = sum[q] * scales[n];
+          if (bias) v = v + bias[n];
+        }
+        v = apply_epi_b16(epi, v);
       }
-      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(apply_epi_b16(epi, v));
+      y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
     }
   }
 }
 
-template <int NP, int TILES, int MB>
-static hipError_t launch_mid_k(const uint16_t *x, const int8_t *Q, const float *scales,
-                               const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
-                               int64_t K, hipStream_t stream) {
+template <int NP, int TILES, int MB, bool GATEUP>
+static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                               const float *scales, const float *scales2, const float *bias,
+                               int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                               hipStream_t stream) {
   constexpr size_t slots = size_t(8) * 2 * 16 * 128;
   constexpr size_t red = size_t(8) * TILES * MB * 64 * sizeof(f32x4);
   constexpr size_t lds = slots > red ? slots : red;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = gemv_w8a16_mid_kernel<NP, TILES, MB>;
+  auto kern = gemv_w8a16_skinny_kernel<NP, TILES, MB, GATEUP>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -895,23 +500,37 @@ static hipError_t launch_mid_k(const uint16_t *x, const int8_t *Q, const float *
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TILES - 1) / (16 * TILES))), dim3(512), lds,
-                     stream, x, Q, scales, bias, epi, y, (int)M, (int)N, (int)K);
+  constexpr int cols = 16 * (GATEUP ? TILES / 2 : TILES);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + cols - 1) / cols)), dim3(512), lds, stream, x, Q,
+                     Q2, scales, scales2, bias, epi, y, (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
 
-// K = 1024 NP (NP <= 4), up to 16 MB x rows
-template <int TILES, int MB>
-static hipError_t launch_mid(const uint16_t *x, const int8_t *Q, const float *scales,
-                             const float *bias, int epi, uint16_t *y, int64_t M, int64_t N,
-                             int64_t K, hipStream_t stream) {
-  switch (K / 1024) {
-    case 1: return launch_mid_k<1, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    case 2: return launch_mid_k<2, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    case 3: return launch_mid_k<3, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    case 4: return launch_mid_k<4, TILES, MB>(x, Q, scales, bias, epi, y, M, N, K, stream);
-    default: return hipErrorInvalidValue;
+// NP = ceil(K / 1024) passes: up to 4 (K <= 4096) for TILES > 1, up to 16
+// (K <= 16384) for one tile per workgroup
+template <int TILES, int MB, bool GATEUP = false>
+static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
+                             const float *scales, const float *scales2, const float *bias,
+                             int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                             hipStream_t stream) {
+  const int np = (int)((K + 1023) / 1024);
+#define MJ_MK(n)                                                                             \
+  case n:                                                                                    \
+    return launch_skinny_k<n, TILES, MB, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, \
+                                              K, stream);
+  if constexpr (TILES > 1) {
+    switch (np) {
+      MJ_MK(1) MJ_MK(2) MJ_MK(3) MJ_MK(4)
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (np) {
+      MJ_MK(5) MJ_MK(6) MJ_MK(7) MJ_MK(8) MJ_MK(9) MJ_MK(10) MJ_MK(11) MJ_MK(12) MJ_MK(13)
+      MJ_MK(14) MJ_MK(15) MJ_MK(16)
+      default: return hipErrorInvalidValue;
+    }
   }
+#undef MJ_MK
 }
 
 // Decode GEMV for one x row (M = 1, K = 1024, 2048, 3072 or 4096): persistent
@@ -1623,28 +1242,24 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
                              int64_t K, hipStream_t stream) {
   if (M == 2 && K <= 16384)
     // 11008 x 4096: 10.1-10.3 us against 11.6-12.3 on the two-rows-per-wave
-    // kernel; 4096 x 11008: 10.1 against 14.4 on the long-K MFMA GEMV
+    // kernel; 4096 x 11008: 10.1 against 14.4 on the MFMA GEMV
     return launch_ksplit_m_k<2, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K,
                                        stream);
-  if (M > 32 && M <= 48 && K % 1024 == 0 && K <= 4096)
-    // 11008 x 4096 at M = 33 / 48 / 64: 20.5-20.9 / 22.6-22.7 / 26.1 us against
-    // 25.4 / 25.7 / 26.3 on the W8A16 tile GEMM (the x reads, M K 2 bytes per
-    // workgroup, grow with M); 32 or 16 weight rows per workgroup: 31.6-59.7 us
-    return launch_mid<3, 4>(x, Q, scales, bias, epi, y, M, N, K, stream);
-  if (M >= kGemvMfmaMinM && M <= 32 && K % 1024 == 0 && K <= 4096) {
+  if (M >= kGemvMfmaMinM && M <= 48 && K % 1024 == 0 && K <= 4096) {
     if (M <= 16)
-      return launch_skinny<3, 8, 1>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
-    return launch_skinny<3, 8, 2>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
+      return launch_skinny<3, 1>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
+    if (M <= 32)
+      return launch_skinny<3, 2>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
+    return launch_skinny<3, 4>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
   }
   if (M >= 3 && M <= 4 && K <= 16384)
-    // 4096 x 11008: 12.6 us against 14.7 on the long-K MFMA GEMV below
+    // 4096 x 11008: 11.3-12.6 us against 13.1 (M = 5) on the skinny GEMV
     return launch_ksplit_m_k<4, false>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K,
                                        stream);
   if (M >= 5 && M <= kGemvMaxM && K > 4096 && K <= 16384)
-    // one 16-row tile per workgroup: 4096 x 11008 at 1 / 2 / 3 tiles (256 / 128
-    // / 86 workgroups) measured 0 / 2.8 / 6.6 us apart over the decode FFN at
-    // M = 16
-    return launch_skinny_long<1>(x, Q, scales, bias, epi, y, M, N, K, stream);
+    // one 16-row tile per workgroup (256 workgroups at N = 4096; 2 or 3 tiles
+    // measured 2.8 and 6.6 us slower over the decode FFN at M = 16)
+    return launch_skinny<1, 1>(x, Q, nullptr, scales, nullptr, bias, epi, y, M, N, K, stream);
   if (M >= kGemvMfmaMinM && M <= kGemvMaxM) {
     // 32-bit buffer offsets over the x rows and the 64 weight rows of a workgroup
     if (M * K * 2 >= ((int64_t)1 << 31) - 64 || 64 * K >= ((int64_t)1 << 31))
@@ -1694,15 +1309,17 @@ hipError_t launch_gemv_gateup_w8a16(const uint16_t *x, const int8_t *Wg, const f
   if (!gemv_gateup_w8a16_takes(M, K)) return hipErrorInvalidValue;
   if (M == 2)  // 2 x 11008 x 4096: 17.3 us against 20.3 on the skinny MFMA GEMV
     return launch_ksplit_m_k<2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
-  if (M <= 4 && (K % 1024 || K > 4096))  // (K = 1024 j <= 4096: 21.5 us here, 20.3 there)
+  if (M <= 4 && (K % 1024 || K > 4096))
     return launch_ksplit_m_k<4, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
-  if (M >= 2) {
+  if (M >= 3) {
     // three gate/up tile pairs (48 columns) per workgroup: the decode FFN
     // (2 x 11008 x 4096 gate/up) at M = 4 measured 51.3 / 50.1 / 45.0 / 45.1 us
-    // with 1 / 2 / 3 / 4 pairs (688 / 344 / 230 / 172 workgroups)
+    // with 1 / 2 / 3 / 4 pairs (688 / 344 / 230 / 172 workgroups) on an
+    // earlier form of the kernel; the FFN at M = 8 / 16 / 32 31.4 / 35.4 /
+    // 42.5 us with 1-KB passes against 33.4 / 38.5 / 47.9 with one 4-KB pass
     if (M <= 16)
-      return launch_skinny<6, 8, 1, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
-    return launch_skinny<6, 8, 2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+      return launch_skinny<6, 1, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
+    return launch_skinny<6, 2, true>(x, Wg, Wu, sg, su, nullptr, 0, h, M, N, K, stream);
   }
   if (K <= 4096)
     return launch_ksplit_g_rw<1, true>(x, Wg, Wu, sg, su, nullptr, 0, h, N, K, stream);

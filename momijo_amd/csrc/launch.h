@@ -108,8 +108,8 @@ hipError_t launch_cast_i64_f32(const int64_t *x, float *y, int64_t n, hipStream_
 // 11008 x 4096 where the 256-row GEMM tile takes 38 us).
 constexpr int64_t kGemvMaxM = 16;
 // Whether launch_gemv_w8a16 takes an M-row W8A16 product: every M <= 16, and
-// 17..48 rows when K = 1024 j <= 4096 (the skinny kernel's two x-row groups up
-// to 32 rows, the batched GEMV's four beyond).
+// 17..48 rows when K = 1024 j <= 4096 (the skinny MFMA GEMV with two or four
+// 16-row x groups).
 inline bool gemv_w8a16_takes(int64_t M, int64_t K) {
   return M <= kGemvMaxM || (M <= 48 && K % 1024 == 0 && K > 0 && K <= 4096);
 }
@@ -118,7 +118,7 @@ hipError_t launch_gemv_w8a16(const uint16_t *x, const int8_t *Q, const float *sc
                              int64_t K, hipStream_t stream);
 // Whether launch_gemv_gateup_w8a16 takes the FFN's gate/up at M x rows: 1..4
 // rows at K % 16 == 0, K <= 16384 (the K-split GEMVs), 5..32 rows at K = 1024 j
-// <= 4096 (the skinny MFMA GEMV).
+// <= 4096 (the skinny MFMA GEMV, which also takes 3..4 rows at such K).
 inline bool gemv_gateup_w8a16_takes(int64_t M, int64_t K) {
   if (K <= 0 || K % 16 || M < 1) return false;
   if (M <= 4) return K <= 16384;
