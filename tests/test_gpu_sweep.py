@@ -214,7 +214,8 @@ def test_sweep_f32_matmul(dev, M, N, K, ta, tb):
 # rounded by the oracle's pinned bf16 rounding; over the two quantizers
 # (per-row RHE / legacy with exact-tie rows, per-tensor legacy with
 # near-ties), bit for bit against the oracle; and over the W8A16 FFN (decode
-# and prefill sizes) against float64 bounds.
+# and prefill sizes) against float64 bounds.  A third of the W8A16 Linear cases
+# take 3-48 x rows at K = 1024 j <= 4096 (the skinny GEMV's range).
 _LONG = float(os.environ.get("MJ_LONG_SWEEP", "0"))
 
 
@@ -240,6 +241,9 @@ def _long_case(rng, fam, dev, to_bf16, oracle_quantize_rowwise=None, oracle_quan
     epi = mj.EPI_RELU if relu else mj.EPI_NONE
     if fam == "w8a16":
         M, N, K = draw_m(), int(rng.integers(1, 12001)), int(rng.integers(1, 1025)) * 16
+        if rng.integers(0, 3) == 0:
+            # the skinny MFMA GEMV's own range: 3-48 x rows at K = 1024 j <= 4096
+            M, K = int(rng.integers(3, 49)), int(rng.integers(1, 5)) * 1024
         N, K = cap(M, N, K, 16)
         x = rng.integers(-2, 3, size=(M, K)).astype(np.float32)
         Q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
