@@ -1442,9 +1442,23 @@ __device__ __forceinline__ void gateup_split_epilogue(const GemmNT &p, const f32
   else run(std::false_type());
 }
 
-template <int BM, int BN, bool GATEUP, int WMT = 128>
+template <int BM, int BN, bool GATEUP, int WMT = 128, int DEPTH = 2>
 __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int NT = 256;
+  // DEPTH 2: stage kt + 2's B loads go out in stage kt's first step (three B
+  // buffers), its A loads in the second (two A buffers).  DEPTH > 2: a ring
+  // of DEPTH stages for A and B alike; stage kt + DEPTH's loads all go out in
+  // stage kt's second step into stage kt's slot (free once the stage's
+  // barrier is passed: its second-step fragments were read in its first
+  // step), so every load has about DEPTH - 1/2 stages to land before the
+  // wait that covers it (loads retire in order: issuing B earlier than A
+  // would not give B more time, since the wait for the A loads issued after
+  // it covers it too).  The weights of a short-M GEMM stream from HBM once,
+  // and two stages in flight left that stream latency-bound; a ring of six
+  // (128 x 128 tiles, 144 KB of LDS) measured between two and three.
+  static_assert(DEPTH == 2 || DEPTH == 3 || DEPTH == 6, "ring depth divides the 6-stage round");
+  constexpr int NA = DEPTH == 2 ? 2 : DEPTH;  // A slots
+  constexpr int NB = DEPTH == 2 ? 3 : DEPTH;  // B slots
   // waves: WMS x WNS, each owning WM x WN (WMT = 128: 2 x 2 on 256-row tiles,
   // 1 x 4 on 128-row ones; WMT = 256: 1 x 4 on 256-row tiles)
   constexpr int WM = WMT, WMS = BM / WM, WNS = 4 / WMS;
@@ -1464,8 +1478,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   constexpr int BROW = 64;                   // int8 B row bytes per stage
   static_assert(BM == 256 || BM == 128, "tile height");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t *As = lds;                                        // [2][BM][64] bf16
-  int8_t *Bs = (int8_t *)(lds + 2 * BM * kBK);               // [3][BN][64] int8
+  uint16_t *As = lds;                                        // [NA][BM][64] bf16
+  int8_t *Bs = (int8_t *)(lds + NA * BM * kBK);              // [NB][BN][64] int8
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1515,7 +1529,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   }
   // direct load d of stage kt: d < 8 is A block d into A buffer abuf, else B
   // block d - 8 into B buffer bbuf.  FAST: the stage lies inside the K slice.
-  auto load = [&](auto fast, int kt, int buf, int d) {
+  auto load = [&](auto fast, int kt, int buf, int d) __attribute__((always_inline)) {
     const int k0 = kt * kBK;
     if (d < A_DPW) {
       uint16_t *dst = As + buf * BM * kBK + (d * 4 + wave) * 8 * kBK;
@@ -1564,11 +1578,14 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   float cvt_lo[4], cvt_hi[4];  // converted int8 pairs awaiting their pack
 
   constexpr int NDMA = A_DPW + B_DPW;
+  constexpr int PRO = DEPTH;  // stages loaded before the loop
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2)
+  for (int s2 = 0; s2 < PRO; ++s2)
 #pragma unroll
     for (int d = 0; d < NDMA; ++d) load(std::false_type(), kt0 + s2, s2, d);
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (NDMA & 0xF) | ((NDMA >> 4) << 14));  // stage kt0
+  constexpr int PW = (PRO - 1) * NDMA;  // loads after stage kt0's
+  static_assert(PW < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (PW & 0xF) | ((PW >> 4) << 14));  // stage kt0
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
   for (int j = 0; j < TN; ++j) fbr[0][j] = ds_read8_asm(b_rd[0] + j * 16 * BROW);
@@ -1598,7 +1615,8 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   // constant, so the fragment arrays stay in registers and the LDS pointers
   // keep their address space.
   auto step = [&](auto src_c, auto dst_c, auto abuf_c, auto bbuf_c, auto fast, int kt,
-                  auto load_d_c, auto nload_c, auto load_buf_c, auto g0_c) {
+                  auto load_d_c, auto nload_c, auto load_buf_c,
+                  auto g0_c) __attribute__((always_inline)) {
     constexpr int src = decltype(src_c)::value, dst = decltype(dst_c)::value;
     constexpr int g0 = decltype(g0_c)::value;  // sequence number of the step's group 0
     constexpr int abuf = decltype(abuf_c)::value, bbuf = decltype(bbuf_c)::value;
@@ -1630,7 +1648,7 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
           const int l = j * lpg + (u - 1);
           if (u == 1 || u == 2 || (u >= 1 && u <= lpg)) {
             __builtin_amdgcn_sched_barrier(0);
-            if (u <= lpg && l < nload) load(fast, kt + 2, load_buf, load_d + l);
+            if (u <= lpg && l < nload) load(fast, kt + DEPTH, load_buf, load_d + l);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -1669,24 +1687,43 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
       }
     }
   };
-  // stage kt in A buffer AB = (kt - kt0) % 2 and B buffer BB = (kt - kt0) % 3
-  auto stage = [&](auto ab_c, auto bb_c, auto pos_c, auto fast, int kt) {
+  // stage kt in A buffer AB = (kt - kt0) % NA and B buffer BB = (kt - kt0) % NB
+  auto stage = [&](auto ab_c, auto bb_c, auto pos_c, auto fast, int kt)
+      __attribute__((always_inline)) {
     constexpr int AB = decltype(ab_c)::value;
     constexpr int BB = decltype(bb_c)::value;
     constexpr int G0 = decltype(pos_c)::value * 2 * TN;  // groups before this stage
-    // step 0; loads of B for stage kt+2 go into B buffer (BB + 2) % 3
-    step(IC<0>(), IC<1>(), IC<AB>(), IC<BB>(), fast, kt, IC<A_DPW>(), IC<B_DPW>(),
-         IC<(BB + 2) % 3>(), IC<G0 % 3>());
+    if constexpr (DEPTH == 2) {
+      // step 0; loads of B for stage kt+2 go into B buffer (BB + 2) % 3
+      step(IC<0>(), IC<1>(), IC<AB>(), IC<BB>(), fast, kt, IC<A_DPW>(), IC<B_DPW>(),
+           IC<(BB + 2) % 3>(), IC<G0 % 3>());
+    } else {
+      step(IC<0>(), IC<1>(), IC<AB>(), IC<BB>(), fast, kt, IC<0>(), IC<0>(), IC<AB>(),
+           IC<G0 % 3>());
+    }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
     for (int j = 1; j < TN; ++j) landed(fbr[1][j]);
-    // only this stage's B loads may be in flight (loads retire in order)
-    __builtin_amdgcn_s_waitcnt(0x0F70 | B_DPW);
+    if constexpr (DEPTH == 2) {
+      // only this stage's B loads may be in flight (loads retire in order)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | B_DPW);
+    } else {
+      // stage kt + 1 landed: the loads of stages kt + 2 .. kt + DEPTH - 1 may
+      // be in flight
+      constexpr int W = (DEPTH - 2) * NDMA;
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (W & 0xF) | ((W >> 4) << 14));
+    }
     asm volatile("s_barrier" ::: "memory");
-    // step 1; loads of A for stage kt+2 go into A buffer AB
-    step(IC<1>(), IC<0>(), IC<AB ^ 1>(), IC<(BB + 1) % 3>(), fast, kt, IC<0>(), IC<A_DPW>(),
-         IC<AB>(), IC<(G0 + TN) % 3>());
+    if constexpr (DEPTH == 2) {
+      // step 1; loads of A for stage kt+2 go into A buffer AB
+      step(IC<1>(), IC<0>(), IC<AB ^ 1>(), IC<(BB + 1) % 3>(), fast, kt, IC<0>(), IC<A_DPW>(),
+           IC<AB>(), IC<(G0 + TN) % 3>());
+    } else {
+      // step 1; all loads of stage kt + DEPTH go into this stage's slot
+      step(IC<1>(), IC<0>(), IC<(AB + 1) % NA>(), IC<(BB + 1) % NB>(), fast, kt, IC<0>(),
+           IC<NDMA>(), IC<AB>(), IC<(G0 + TN) % 3>());
+    }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
@@ -1697,26 +1734,47 @@ __global__ __launch_bounds__(256) void gemm_nt_w4i8_kernel(GemmNT p) {
   using I2 = std::integral_constant<int, 2>;
   using F = std::true_type;
   using S = std::false_type;
-  // stages kt .. kt+5 load stages kt+2 .. kt+7: fast while those lie inside K
+  // stages kt .. kt+5 load stages kt+DEPTH .. kt+5+DEPTH: fast while those lie inside K
   const int full_end = kt0 + (Kend - kt0 * kBK) / kBK;  // stages wholly inside the slice
   int kt = kt0;
   // (the third argument is the stage's position in the 6-stage round, which
   // fixes the rotation of the widened-fragment registers)
-  for (; kt + 8 <= full_end; kt += 6) {
-    stage(I0(), I0(), IC<0>(), F(), kt);
-    stage(I1(), I1(), IC<1>(), F(), kt + 1);
-    stage(I0(), I2(), IC<2>(), F(), kt + 2);
-    stage(I1(), I0(), IC<3>(), F(), kt + 3);
-    stage(I0(), I1(), IC<4>(), F(), kt + 4);
-    stage(I1(), I2(), IC<5>(), F(), kt + 5);
-  }
-  for (; kt < kt1; kt += 6) {
-    stage(I0(), I0(), IC<0>(), S(), kt);
-    if (kt + 1 < kt1) stage(I1(), I1(), IC<1>(), S(), kt + 1);
-    if (kt + 2 < kt1) stage(I0(), I2(), IC<2>(), S(), kt + 2);
-    if (kt + 3 < kt1) stage(I1(), I0(), IC<3>(), S(), kt + 3);
-    if (kt + 4 < kt1) stage(I0(), I1(), IC<4>(), S(), kt + 4);
-    if (kt + 5 < kt1) stage(I1(), I2(), IC<5>(), S(), kt + 5);
+  if constexpr (DEPTH == 2) {
+    for (; kt + 8 <= full_end; kt += 6) {
+      stage(I0(), I0(), IC<0>(), F(), kt);
+      stage(I1(), I1(), IC<1>(), F(), kt + 1);
+      stage(I0(), I2(), IC<2>(), F(), kt + 2);
+      stage(I1(), I0(), IC<3>(), F(), kt + 3);
+      stage(I0(), I1(), IC<4>(), F(), kt + 4);
+      stage(I1(), I2(), IC<5>(), F(), kt + 5);
+    }
+    for (; kt < kt1; kt += 6) {
+      stage(I0(), I0(), IC<0>(), S(), kt);
+      if (kt + 1 < kt1) stage(I1(), I1(), IC<1>(), S(), kt + 1);
+      if (kt + 2 < kt1) stage(I0(), I2(), IC<2>(), S(), kt + 2);
+      if (kt + 3 < kt1) stage(I1(), I0(), IC<3>(), S(), kt + 3);
+      if (kt + 4 < kt1) stage(I0(), I1(), IC<4>(), S(), kt + 4);
+      if (kt + 5 < kt1) stage(I1(), I2(), IC<5>(), S(), kt + 5);
+    }
+  } else {
+    // slot (kt - kt0) % DEPTH; DEPTH divides the 6-stage round
+    constexpr int R = DEPTH;
+    for (; kt + 6 + DEPTH <= full_end; kt += 6) {
+      stage(IC<0 % R>(), IC<0 % R>(), IC<0>(), F(), kt);
+      stage(IC<1 % R>(), IC<1 % R>(), IC<1>(), F(), kt + 1);
+      stage(IC<2 % R>(), IC<2 % R>(), IC<2>(), F(), kt + 2);
+      stage(IC<3 % R>(), IC<3 % R>(), IC<3>(), F(), kt + 3);
+      stage(IC<4 % R>(), IC<4 % R>(), IC<4>(), F(), kt + 4);
+      stage(IC<5 % R>(), IC<5 % R>(), IC<5>(), F(), kt + 5);
+    }
+    for (; kt < kt1; kt += 6) {
+      stage(IC<0 % R>(), IC<0 % R>(), IC<0>(), S(), kt);
+      if (kt + 1 < kt1) stage(IC<1 % R>(), IC<1 % R>(), IC<1>(), S(), kt + 1);
+      if (kt + 2 < kt1) stage(IC<2 % R>(), IC<2 % R>(), IC<2>(), S(), kt + 2);
+      if (kt + 3 < kt1) stage(IC<3 % R>(), IC<3 % R>(), IC<3>(), S(), kt + 3);
+      if (kt + 4 < kt1) stage(IC<4 % R>(), IC<4 % R>(), IC<4>(), S(), kt + 4);
+      if (kt + 5 < kt1) stage(IC<5 % R>(), IC<5 % R>(), IC<5>(), S(), kt + 5);
+    }
   }
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1889,10 +1947,11 @@ static hipError_t launch_tile(const GemmNT &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, bool GATEUP, int WMT = 128>
+template <int BM, int BN, bool GATEUP, int WMT = 128, int DEPTH = 2>
 static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   constexpr int BN_OUT = GATEUP ? BN / 2 : BN;
-  constexpr size_t lds_loop = size_t(2) * BM * kBK * sizeof(uint16_t) + size_t(3) * BN * 64;
+  constexpr int NA = DEPTH == 2 ? 2 : DEPTH, NB = DEPTH == 2 ? 3 : DEPTH;
+  constexpr size_t lds_loop = size_t(NA) * BM * kBK * sizeof(uint16_t) + size_t(NB) * BN * 64;
   constexpr size_t lds_out = size_t(BM) * stage_ld<BN_OUT>() * sizeof(uint16_t);
   // the split gate/up epilogue's two fp32 exchange regions (128 rows each)
   constexpr size_t lds_x = GATEUP ? size_t(2) * (WMT / 2) * (BN_OUT + 4) * 4 : 0;
@@ -1904,7 +1963,7 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   if (p.K >= ((int64_t)1 << 30) || p.bkind != B_INT8 || p.gate_up != GATEUP ||
       p.N * p.ldb >= ((int64_t)1 << 31) || BM * p.lda * 2 >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
-  auto kern = gemm_nt_w4i8_kernel<BM, BN, GATEUP, WMT>;
+  auto kern = gemm_nt_w4i8_kernel<BM, BN, GATEUP, WMT, DEPTH>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -1919,6 +1978,14 @@ static hipError_t launch_w4i8(const GemmNT &p, hipStream_t stream) {
   if (grid > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, stream, p);
   return hipGetLastError();
+}
+
+// The W8A16 tile kernel with the plan's load depth (2, or the 3-stage ring).
+template <int BM, int BN, bool GATEUP, int WMT>
+static hipError_t launch_w4i8_d(const GemmNT &p, int depth, hipStream_t stream) {
+  if (depth == 3) return launch_w4i8<BM, BN, GATEUP, WMT, 3>(p, stream);
+  if (depth != 2) return hipErrorInvalidValue;
+  return launch_w4i8<BM, BN, GATEUP, WMT>(p, stream);
 }
 
 template <int BKIND, bool IGLP, bool PF2>
@@ -1990,6 +2057,17 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
   // the one-wave-per-SIMD int8 kernel needs 31-bit weight offsets and K < 2^30
   const bool w4i8_ok = p.bkind == B_INT8 && p.K < ((int64_t)1 << 30) &&
                        p.N * p.ldb < ((int64_t)1 << 31) && 256 * p.lda * 2 < ((int64_t)1 << 31);
+  // Up to 256 x rows (one row tile) every weight tile streams from HBM once,
+  // and with two stages of loads in flight that stream was latency-bound: a
+  // ring of three stages (all of a stage's loads in the second step of the
+  // stage three earlier) took, on MI355X, the W8A16 GEMM 11008 x 4096 at M =
+  // 64 / 128 / 192 / 256 from 26.7 / 29.1 / 35.3 / 37.8 to 24.5 / 27.0 / 34.8
+  // / 36.5 us and the FFN 4096 -> 11008 -> 4096 at M = 64 / 128 / 256 from
+  // 66.1 / 68.8 / 88.5 to 60.3 / 61.9 / 86.0 us (bit-identical sums).  Where
+  // the weight tiles are re-read by several row tiles (C4, C5) it was 0.5-1 %
+  // slower (C4 1245-1248 -> 1236-1241 TFLOP/s, C5 1154-1158 -> 1146-1151,
+  // alternating bench runs on one box), so those keep two stages.
+  const int depth = p.M <= 256 ? 3 : 2;
   if (p.gate_up) {
     // The one-wave-per-SIMD int8 kernel in its split layout: 1 x 4 waves of
     // BM x BN/4, gate rows in waves 0-1 and the up rows of the same columns
@@ -2011,6 +2089,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     if (pl.tile_kernel) {
       pl.wm = p.M <= 128 ? 128 : 256;
       pl.bm = pl.wm;
+      pl.depth = depth;
       const int64_t tm = (p.M + 255) / 256;
       const int64_t r256 = (tm * ((p.N + 127) / 128) + 255) / 256;
       const int64_t r192 = (tm * ((p.N + 95) / 96) + 255) / 256;
@@ -2030,6 +2109,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     pl.bm = p.M <= 128 ? 128 : 256;
     pl.bn = 128;
     pl.wm = pl.bm;
+    pl.depth = depth;
     pl.tile_kernel = true;
     const int64_t tiles = ((p.M + pl.bm - 1) / pl.bm) * ((p.N + 127) / 128);
     const int64_t nk = (p.K + kBK - 1) / kBK;
@@ -2053,6 +2133,7 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     pl.bm = 256;
     pl.bn = 128;
     pl.wm = 256;
+    pl.depth = depth;
     pl.tile_kernel = true;
     const int64_t tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
     const int64_t nk = (p.K + kBK - 1) / kBK;
@@ -2096,14 +2177,14 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
     if (pl.iglp || pl.pf2) return hipErrorInvalidValue;
     if (pl.tile_kernel) {
       if (pl.bm == 128 && pl.wm == 128) {
-        if (pl.bn == 128) return launch_w4i8<128, 128, true, 128>(p, stream);
-        if (pl.bn == 192) return launch_w4i8<128, 192, true, 128>(p, stream);
-        return launch_w4i8<128, 256, true, 128>(p, stream);
+        if (pl.bn == 128) return launch_w4i8_d<128, 128, true, 128>(p, pl.depth, stream);
+        if (pl.bn == 192) return launch_w4i8_d<128, 192, true, 128>(p, pl.depth, stream);
+        return launch_w4i8_d<128, 256, true, 128>(p, pl.depth, stream);
       }
       if (pl.bm != 256 || pl.wm != 256) return hipErrorInvalidValue;
-      if (pl.bn == 128) return launch_w4i8<256, 128, true, 256>(p, stream);
-      if (pl.bn == 192) return launch_w4i8<256, 192, true, 256>(p, stream);
-      if (pl.bn == 256) return launch_w4i8<256, 256, true, 256>(p, stream);
+      if (pl.bn == 128) return launch_w4i8_d<256, 128, true, 256>(p, pl.depth, stream);
+      if (pl.bn == 192) return launch_w4i8_d<256, 192, true, 256>(p, pl.depth, stream);
+      if (pl.bn == 256) return launch_w4i8_d<256, 256, true, 256>(p, pl.depth, stream);
       return hipErrorInvalidValue;
     }
     if (pl.bm == 256) return launch_tile<256, 256, B_INT8, true, false>(p, stream);
@@ -2131,10 +2212,10 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
       e = launch_tile<128, 256, B_BF16, false, true, true>(p, stream);
   } else if (pl.tile_kernel) {
     if (pl.bm == 128 && pl.bn == 128 && pl.wm == 128) {
-      e = launch_w4i8<128, 128, false, 128>(p, stream);
+      e = launch_w4i8_d<128, 128, false, 128>(p, pl.depth, stream);
     } else {
       if (pl.bm != 256 || pl.bn != 128 || pl.wm != 256) return hipErrorInvalidValue;
-      e = launch_w4i8<256, 128, false, 256>(p, stream);
+      e = launch_w4i8_d<256, 128, false, 256>(p, pl.depth, stream);
     }
   } else {
     if (pl.pf2) return hipErrorInvalidValue;

@@ -42,6 +42,8 @@ struct GemmPlan {
   int wm = 128;              // W8A16 tile kernels: wave tile height; the planner sets 256
                              // (1 x 4 waves of 256 rows: each widened B fragment feeds 16
                              // MFMAs)
+  int depth = 2;             // W8A16 tile kernels: stages of loads in flight (2, or a ring of
+                             // 3 where the weights stream from HBM once: M <= 256)
   size_t workspace_bytes(const GemmNT &p) const {
     return splits > 1 ? (size_t)splits * (size_t)p.M * (size_t)p.N * sizeof(float) : 0;
   }
