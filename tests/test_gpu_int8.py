@@ -379,16 +379,23 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    (2, 4096, 11008), (2, 20000, 6000), (2, 11008, 4096),
                                    (3, 4096, 11008), (4, 37, 5008), (4, 1000, 16384),
                                    (4, 300, 1040),
-                                   # 5-16 x rows, 4096 < K <= 16384: the long-K
-                                   # skinny MFMA GEMV, 2-4 passes (the last one
-                                   # 1-4 KB and past K), partial tiles
+                                   # 5-16 x rows, 4096 < K <= 16384: the skinny
+                                   # MFMA GEMV with one tile per workgroup, 5-16
+                                   # passes of 1 KB (the last one past K),
+                                   # partial tiles
                                    (5, 300, 5008), (9, 37, 12304), (16, 4100, 8192),
                                    (16, 1000, 16384),
-                                   # 33-48 x rows at K = 1024 j: the batched
+                                   # 33-48 x rows at K = 1024 j: the skinny
                                    # GEMV's four x-row groups over 1-KB passes
                                    # (64: the tile GEMM again)
                                    (33, 300, 1024), (40, 37, 2048), (48, 4100, 4096),
-                                   (48, 11008, 4096), (64, 1000, 3072)])
+                                   (48, 11008, 4096), (64, 1000, 3072),
+                                   # M <= 256 on the tile GEMM's three-stage
+                                   # load ring: K slices of one, two and three
+                                   # stages (shorter than the ring), a partial
+                                   # last stage, 128- and 256-row tiles
+                                   (64, 300, 64), (100, 520, 128), (128, 130, 176),
+                                   (200, 260, 192), (256, 1000, 336), (255, 4100, 4096)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
@@ -525,6 +532,9 @@ def test_c5_mlp(oracle, dev):
                                    # 33-128 x rows: the gate/up GEMM's narrow tiles
                                    (33, 1024, 1008), (64, 4096, 11008), (128, 1040, 720),
                                    (200, 1024, 2000), (256, 4096, 11008),
+                                   # K of one and two stages, shorter than the
+                                   # three-stage load ring of M <= 256
+                                   (64, 64, 272), (200, 128, 400),
                                    # 2-4 x rows: the two- and four-row K-split
                                    # GEMVs' gate/up
                                    (2, 4096, 11008), (2, 1040, 400), (3, 5008, 304),
