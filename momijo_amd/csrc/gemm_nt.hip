@@ -569,7 +569,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; j += 2) {
+    for (int j = 0; j + 1 < TN; j += 2) {
       float x[4], y[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -584,6 +584,18 @@ __device__ __forceinline__ void store_tile_direct(const GemmNT &p, const f32x4 (
       const int m = m0 + wm * WM + i * 16 + fr;
       const int n = n0 + wn * WN + (j + (fh & 1)) * 16 + 8 * (fh >> 1);
       *(uint4 *)(p.C + (size_t)m * p.ldc + n) = make_uint4(w0[0], w1[0], w0[1], w1[1]);
+    }
+    if constexpr (TN % 2 == 1) {
+      // an odd last block: its 4 columns per lane as one 8-byte store
+      float x[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        x[q] = apply_epi_b16(E, epi_scale_bias(acc[i][TN - 1][q], s[TN - 1][q], b[TN - 1][q],
+                                               has_s, has_b));
+      const int m = m0 + wm * WM + i * 16 + fr;
+      const int n = n0 + wn * WN + (TN - 1) * 16 + 4 * fh;
+      *(uint2 *)(p.C + (size_t)m * p.ldc + n) = make_uint2(pack_bf16x2(x[0], x[1]),
+                                                           pack_bf16x2(x[2], x[3]));
     }
   }
 }
@@ -2111,10 +2123,29 @@ GemmPlan plan_gemm_nt(const GemmNT &p) {
     pl.wm = pl.bm;
     pl.depth = depth;
     pl.tile_kernel = true;
-    const int64_t tiles = ((p.M + pl.bm - 1) / pl.bm) * ((p.N + 127) / 128);
     const int64_t nk = (p.K + kBK - 1) / kBK;
-    while (pl.splits < 8 && tiles * pl.splits * 2 <= 256 && nk / (pl.splits * 2) >= 8)
-      pl.splits *= 2;
+    // K split until the grid covers the CUs; the share of the CU rounds the
+    // grid keeps busy
+    auto fill = [&](int bn, int &splits) {
+      const int64_t tiles = ((p.M + pl.bm - 1) / pl.bm) * ((p.N + bn - 1) / bn);
+      splits = 1;
+      while (splits < 8 && tiles * splits * 2 <= 256 && nk / (splits * 2) >= 8) splits *= 2;
+      const int64_t wgs = tiles * splits;
+      return (double)wgs / (256.0 * (double)((wgs + 255) / 256));
+    };
+    int s128 = 1, s192 = 1;
+    const double f128 = fill(128, s128);
+    pl.splits = s128;
+    // 128-row tiles 192 columns wide where they fill more of the chip
+    // (waves of 128 x 48): 11008 x 4096 at M = 64 / 128 on 58 tiles x 4 K
+    // slices (232 workgroups) 22.6-22.7 / 26.1-26.3 us against 24.2-24.4 /
+    // 26.5-26.7 on 86 x 2 (172), MI355X, alternating runs on one box; at
+    // 4096 x 11008 the 128-column tiles' 32 x 8 (256) stay (21.4 / 25.0
+    // against 23.6 / 27.1 us on 22 x 8)
+    if (pl.bm == 128 && fill(192, s192) > f128 + 0.05) {
+      pl.bn = 192;
+      pl.splits = s192;
+    }
     return pl;
   }
   if (w4i8_ok && p.M >= 256) {
@@ -2213,6 +2244,8 @@ hipError_t launch_gemm_nt(const GemmNT &p_in, const GemmPlan &pl, hipStream_t st
   } else if (pl.tile_kernel) {
     if (pl.bm == 128 && pl.bn == 128 && pl.wm == 128) {
       e = launch_w4i8_d<128, 128, false, 128>(p, pl.depth, stream);
+    } else if (pl.bm == 128 && pl.bn == 192 && pl.wm == 128) {
+      e = launch_w4i8_d<128, 192, false, 128>(p, pl.depth, stream);
     } else {
       if (pl.bm != 256 || pl.bn != 128 || pl.wm != 256) return hipErrorInvalidValue;
       e = launch_w4i8_d<256, 128, false, 256>(p, pl.depth, stream);

@@ -37,8 +37,9 @@ struct GemmPlan {
   bool iglp = false;  // K loop built with the compiler's MFMA interleave
   bool pf2 = false;   // distance-2 load pipeline (bf16 B)
   bool tile_kernel = false;  // the dedicated tile kernels: bf16 256 x 256 (two waves per
-                             // SIMD), W8A16 256 x 128, gate/up 128 or 256 rows x 128,
-                             // 192 or 256 (one wave per SIMD)
+                             // SIMD), W8A16 256 x 128 (128 x 128 or 128 x 192 up to 128
+                             // rows), gate/up 128 or 256 rows x 128, 192 or 256 (one wave
+                             // per SIMD)
   int wm = 128;              // W8A16 tile kernels: wave tile height; the planner sets 256
                              // (1 x 4 waves of 256 rows: each widened B fragment feeds 16
                              // MFMAs)

@@ -395,7 +395,12 @@ def test_w8a16_gemm_shapes(oracle, dev, M, N, K):
                                    # stages (shorter than the ring), a partial
                                    # last stage, 128- and 256-row tiles
                                    (64, 300, 64), (100, 520, 128), (128, 130, 176),
-                                   (200, 260, 192), (256, 1000, 336), (255, 4100, 4096)])
+                                   (200, 260, 192), (256, 1000, 336), (255, 4100, 4096),
+                                   # 128 x 192 tiles where they fill more CUs:
+                                   # 27 tiles x 8 K slices; 209 unsplit tiles
+                                   # (full ones store their odd third block
+                                   # directly, a partial last column tile)
+                                   (64, 5000, 4096), (128, 40000, 256)])
 def test_w8a16_integer_inputs_bit_exact(oracle, dev, M, N, K):
     """Small-integer activations, int8 weights and power-of-two scales make
     every product and partial sum exact in fp32 (|sum| <= 4 * 127 * K < 2^24),
