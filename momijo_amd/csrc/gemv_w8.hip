@@ -299,8 +299,9 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F
 // The x fragments of all MB groups for a pass sit in registers, in two sets:
 // the next pass's loads are issued just before its first weight loads (one
 // wait then covers both: loads retire in order) while the current pass still
-// reads the other set.  Two steps in flight; no barrier in the loop (a wave
-// reads only its own region).  Past K (K rounded up to 1 KB) the x fragments
+// reads the other set.  Two steps in flight (DS; four with one tile per
+// workgroup, where every step opens a pass and the x sets rotate with the
+// steps); no barrier in the loop (a wave reads only its own region).  Past K (K rounded up to 1 KB) the x fragments
 // load zero and the weight bytes there (the next row's, or zero past the
 // buffer) add exact zeros.  The eight waves' partial tiles are added in K
 // order through LDS (deterministic), then scale, bias and the activation.
@@ -315,7 +316,7 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F
 // grows).  The FFN's down projection (4096 x 11008, one tile per workgroup) at
 // M = 5 / 8 / 16: 13.1-13.2 / 13.7-13.8 / 16.7 us against 14.0 / 14.5 / 18.2
 // with 4-KB passes.
-template <int NP, int TILES, int MB, bool GATEUP>
+template <int NP, int TILES, int MB, bool GATEUP, int DS = 2>
 __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
     const uint16_t *__restrict__ x, const int8_t *__restrict__ Q, const int8_t *__restrict__ Q2,
     const float *__restrict__ scales, const float *__restrict__ scales2,
@@ -329,6 +330,10 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
   constexpr int XL = 2 * MB * NJ;  // x loads per pass
   constexpr int TP = GATEUP ? TILES / 2 : TILES;  // 16-column output tiles
   static_assert(!GATEUP || TILES % 2 == 0, "gate/up tiles come in pairs");
+  // DS steps in flight; more than two only with one tile per workgroup,
+  // where every step opens a pass (x sets rotate with the steps)
+  static_assert(DS == 2 || (DS > 2 && TILES == 1), "steps in flight");
+  constexpr int XS = TILES == 1 ? DS : 2;  // x fragment sets
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (int64_t)M * K * 2);
   uint8_t *mine = lds8 + wave * 2 * SLOT;
 
-  uint4 xa[2][MB][NJ], xb[2][MB][NJ];
+  uint4 xa[XS][MB][NJ], xb[XS][MB][NJ];
   // x fragments of pass p into set p & 1: group g, block j: x row 16 g + r,
   // k = 1024 p + KQ wave + 64 j + 16 c .. + 15 (zero past M or K; K % 16 == 0
   // keeps a fragment all in or all out).  Past K the weight bytes (the next
@@ -357,11 +362,11 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
         const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
         const u32x4 b =
             __builtin_amdgcn_raw_buffer_load_b128(rx, xo == kOobOffset ? xo : xo + 16, 0, 0);
-        xa[p & 1][g][j] = make_uint4(a[0], a[1], a[2], a[3]);
-        xb[p & 1][g][j] = make_uint4(b[0], b[1], b[2], b[3]);
+        xa[p % XS][g][j] = make_uint4(a[0], a[1], a[2], a[3]);
+        xb[p % XS][g][j] = make_uint4(b[0], b[1], b[2], b[3]);
       }
   };
-  uint4 R[2][CP];
+  uint4 R[DS][CP];
   // step st = (pass p, tile t): load i, lane l holds LDS byte e = 1024 i + 16 l
   // of the wave's region, row e / KQ, chunk (e % KQ) / 16 from global chunk
   // chunk ^ (row & 7).  GATEUP: tile 2 j is gate rows 16 j.., tile 2 j + 1
@@ -377,15 +382,17 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
           (uint32_t)((tr * 16 + rr) * K + 1024 * p + wave * KQ + 16 * (ch ^ (rr & 7)));
       const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((GATEUP && (t & 1)) ? rQ2 : rQ,
                                                             off, 0, 2 /* nt */);
-      R[st & 1][i] = make_uint4(v[0], v[1], v[2], v[3]);
+      R[st % DS][i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
   };
   load_x(0);
   issue(0);
-  if (STEPS > 1) {
-    if (TILES == 1) load_x(1);
-    issue(1);
-  }
+#pragma unroll
+  for (int d = 1; d < DS; ++d)
+    if (d < STEPS) {
+      if (TILES == 1) load_x(d);
+      issue(d);
+    }
   f32x4 acc[TILES][MB];
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
@@ -394,18 +401,27 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
     const int p = st / TILES, t = st % TILES;
-    // step st landed (and its pass's x): at most step st + 1's loads, and the
-    // x loads of the pass it opens, still outstanding
-    if (st + 1 < STEPS) {
-      if ((st + 1) % TILES == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP + XL));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP));
+    // step st landed (and its pass's x): at most the loads of the steps
+    // after it (and the x loads of the passes they open) still outstanding
+    if constexpr (DS == 2) {
+      if (st + 1 < STEPS) {
+        if ((st + 1) % TILES == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP + XL));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP));
+      } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      }
     } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      // one tile: every step is CP weight loads and XL x loads
+      const int after = STEPS - 1 - st < DS - 1 ? STEPS - 1 - st : DS - 1;
+      if (after >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * (CP + XL)));
+      else if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (CP + XL)));
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP + XL));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < CP; ++i)
-      *(uint4 *)(mine + (st & 1) * SLOT + 1024 * i + 16 * lane) = R[st & 1][i];
+      *(uint4 *)(mine + (st & 1) * SLOT + 1024 * i + 16 * lane) = R[st % DS][i];
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("" ::: "memory");
     const uint8_t *src = mine + (st & 1) * SLOT + r * KQ;
@@ -419,17 +435,17 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
 #pragma unroll
       for (int g = 0; g < MB; ++g) {
         acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w0, __builtin_bit_cast(bf16x8, xa[p & 1][g][j]), acc[t][g], 0, 0, 0);
+            w0, __builtin_bit_cast(bf16x8, xa[p % XS][g][j]), acc[t][g], 0, 0, 0);
         acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            w1, __builtin_bit_cast(bf16x8, xb[p & 1][g][j]), acc[t][g], 0, 0, 0);
+            w1, __builtin_bit_cast(bf16x8, xb[p % XS][g][j]), acc[t][g], 0, 0, 0);
       }
     }
-    if (st + 2 < STEPS) {
+    if (st + DS < STEPS) {
       // this wave's fragment reads of the region are done before it is refilled
       __builtin_amdgcn_s_waitcnt(0xC07F);
       asm volatile("" ::: "memory");
-      if ((st + 2) % TILES == 0) load_x((st + 2) / TILES);
-      issue(st + 2);
+      if ((st + DS) % TILES == 0) load_x((st + DS) / TILES);
+      issue(st + DS);
     }
   }
   __syncthreads();
@@ -480,7 +496,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
   }
 }
 
-template <int NP, int TILES, int MB, bool GATEUP>
+template <int NP, int TILES, int MB, bool GATEUP, int DS = 2>
 static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
                                const float *scales, const float *scales2, const float *bias,
                                int epi, uint16_t *y, int64_t M, int64_t N, int64_t K,
@@ -489,7 +505,7 @@ static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8
   constexpr size_t red = size_t(8) * TILES * MB * 64 * sizeof(f32x4);
   constexpr size_t lds = slots > red ? slots : red;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = gemv_w8a16_skinny_kernel<NP, TILES, MB, GATEUP>;
+  auto kern = gemv_w8a16_skinny_kernel<NP, TILES, MB, GATEUP, DS>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
@@ -507,7 +523,10 @@ static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8
 }
 
 // NP = ceil(K / 1024) passes: up to 4 (K <= 4096) for TILES > 1, up to 16
-// (K <= 16384) for one tile per workgroup
+// (K <= 16384) for one tile per workgroup, with four steps (passes) in flight
+// there: the FFN's down projection 4096 x 11008 at M = 5 / 8 / 16 13.3 / 13.7
+// / 16.9 -> 12.6 / 13.1 / 15.8 us against two (three: 13.0 / 13.3 / 16.3),
+// alternating runs on one box on MI355X
 template <int TILES, int MB, bool GATEUP = false>
 static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
                              const float *scales, const float *scales2, const float *bias,
@@ -516,8 +535,8 @@ static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t
   const int np = (int)((K + 1023) / 1024);
 #define MJ_MK(n)                                                                             \
   case n:                                                                                    \
-    return launch_skinny_k<n, TILES, MB, GATEUP>(x, Q, Q2, scales, scales2, bias, epi, y, M, N, \
-                                              K, stream);
+    return launch_skinny_k<n, TILES, MB, GATEUP, TILES == 1 ? 4 : 2>(                         \
+        x, Q, Q2, scales, scales2, bias, epi, y, M, N, K, stream);
   if constexpr (TILES > 1) {
     switch (np) {
       MJ_MK(1) MJ_MK(2) MJ_MK(3) MJ_MK(4)
