@@ -299,9 +299,10 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x0F
 // The x fragments of all MB groups for a pass sit in registers, in two sets:
 // the next pass's loads are issued just before its first weight loads (one
 // wait then covers both: loads retire in order) while the current pass still
-// reads the other set.  Two steps in flight (DS; four with one tile per
-// workgroup, where every step opens a pass and the x sets rotate with the
-// steps); no barrier in the loop (a wave reads only its own region).  Past K (K rounded up to 1 KB) the x fragments
+// reads the other set.  DS steps in flight (at most TILES + 1, so that no
+// more than two passes are; with one tile per workgroup every step opens a
+// pass and DS x sets rotate with the steps); no barrier in the loop (a wave
+// reads only its own region).  Past K (K rounded up to 1 KB) the x fragments
 // load zero and the weight bytes there (the next row's, or zero past the
 // buffer) add exact zeros.  The eight waves' partial tiles are added in K
 // order through LDS (deterministic), then scale, bias and the activation.
@@ -332,8 +333,8 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
   static_assert(!GATEUP || TILES % 2 == 0, "gate/up tiles come in pairs");
   // DS steps in flight; more than two only with one tile per workgroup,
   // where every step opens a pass (x sets rotate with the steps)
-  static_assert(DS == 2 || (DS > 2 && TILES == 1), "steps in flight");
-  constexpr int XS = TILES == 1 ? DS : 2;  // x fragment sets
+  static_assert(DS >= 2 && (TILES == 1 || DS <= TILES + 1), "steps in flight");
+  constexpr int XS = TILES == 1 ? DS : 2;  // x fragment sets (passes in flight)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -390,7 +391,7 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
 #pragma unroll
   for (int d = 1; d < DS; ++d)
     if (d < STEPS) {
-      if (TILES == 1) load_x(d);
+      if (d % TILES == 0) load_x(d / TILES);  // step d opens pass d / TILES
       issue(d);
     }
   f32x4 acc[TILES][MB];
@@ -411,12 +412,22 @@ __global__ __launch_bounds__(512) void gemv_w8a16_skinny_kernel(
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
     } else {
-      // one tile: every step is CP weight loads and XL x loads
-      const int after = STEPS - 1 - st < DS - 1 ? STEPS - 1 - st : DS - 1;
-      if (after >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * (CP + XL)));
-      else if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (CP + XL)));
-      else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CP + XL));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      // the loads of steps st + 1 .. st + DS - 1 (CP each, plus XL x loads
+      // for a step that opens a pass); st is a constant once unrolled, so
+      // the switch folds to one wait
+      int n = 0;
+#pragma unroll
+      for (int d = 1; d < DS; ++d)
+        if (st + d < STEPS) n += CP + ((st + d) % TILES == 0 ? XL : 0);
+      switch (n) {
+#define MJ_W(c) case c: __builtin_amdgcn_s_waitcnt(vmcnt_imm(c)); break;
+        MJ_W(0) MJ_W(1) MJ_W(2) MJ_W(3) MJ_W(4) MJ_W(5) MJ_W(6) MJ_W(7) MJ_W(8) MJ_W(9)
+        MJ_W(10) MJ_W(11) MJ_W(12) MJ_W(13) MJ_W(14) MJ_W(15) MJ_W(16) MJ_W(17) MJ_W(18)
+        MJ_W(19) MJ_W(20) MJ_W(21) MJ_W(22) MJ_W(23) MJ_W(24) MJ_W(25) MJ_W(26) MJ_W(27)
+        MJ_W(28) MJ_W(29) MJ_W(30) MJ_W(31) MJ_W(32)
+#undef MJ_W
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+      }
     }
     asm volatile("" ::: "memory");
 #pragma unroll
@@ -523,10 +534,13 @@ static hipError_t launch_skinny_k(const uint16_t *x, const int8_t *Q, const int8
 }
 
 // NP = ceil(K / 1024) passes: up to 4 (K <= 4096) for TILES > 1, up to 16
-// (K <= 16384) for one tile per workgroup, with four steps (passes) in flight
-// there: the FFN's down projection 4096 x 11008 at M = 5 / 8 / 16 13.3 / 13.7
-// / 16.9 -> 12.6 / 13.1 / 15.8 us against two (three: 13.0 / 13.3 / 16.3),
-// alternating runs on one box on MI355X
+// (K <= 16384) for one tile per workgroup.  Four steps in flight: against two,
+// alternating runs on one box on MI355X, the FFN's down projection 4096 x
+// 11008 at M = 5 / 8 / 16 13.3 / 13.7 / 16.9 -> 12.6 / 13.1 / 15.8 us (one
+// tile; three steps: 13.0 / 13.3 / 16.3), 11008 x 4096 at M = 4 / 16 / 32 /
+// 48 11.0-11.1 / 12.3 / 16.8 / 22.3 -> 10.8-10.9 / 12.4-12.6 / 16.1-16.2 /
+// 21.4-21.5 us, the decode FFN at M = 4 / 16 30.4 / 35.8-37.1 -> 29.9 /
+// 35.1-35.2 us
 template <int TILES, int MB, bool GATEUP = false>
 static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t *Q2,
                              const float *scales, const float *scales2, const float *bias,
@@ -535,8 +549,8 @@ static hipError_t launch_skinny(const uint16_t *x, const int8_t *Q, const int8_t
   const int np = (int)((K + 1023) / 1024);
 #define MJ_MK(n)                                                                             \
   case n:                                                                                    \
-    return launch_skinny_k<n, TILES, MB, GATEUP, TILES == 1 ? 4 : 2>(                         \
-        x, Q, Q2, scales, scales2, bias, epi, y, M, N, K, stream);
+    return launch_skinny_k<n, TILES, MB, GATEUP, 4>(x, Q, Q2, scales, scales2, bias, epi, y, M, \
+                                                    N, K, stream);
   if constexpr (TILES > 1) {
     switch (np) {
       MJ_MK(1) MJ_MK(2) MJ_MK(3) MJ_MK(4)
