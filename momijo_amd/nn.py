@@ -223,9 +223,10 @@ class W8Linear:
     per-channel generalisation of QuantLinear's weights, applied to the
     reference's Linear layout [OutF, InF].
 
-    y = bf16(epi((x . q^T) * scale[n] + bias[n])); M <= 16 rows (M <= 32
-    when K is a multiple of 1024 up to 4096) take the GEMV kernels (streaming
-    for M <= 2, skinny MFMA above), more rows the MFMA GEMM."""
+    y = bf16(epi((x . q^T) * scale[n] + bias[n])); M <= 16 rows (M <= 48
+    when K is a multiple of 1024 up to 4096) take the GEMV kernels (K-split
+    streaming for M <= 2 and for 3-4 rows at other K, skinny MFMA otherwise),
+    more rows the MFMA GEMM."""
 
     def __init__(self, q: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None,
                  epi: int = _lib.EPI_NONE):
