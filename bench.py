@@ -255,7 +255,8 @@ def bench_c3_batch(steps, warmup):
             "metric": f"int8 weight-only GEMV GB/s (M={M})",
             "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                         "frac": gbs / PEAK_HBM_GBS,
+                         "traffic": _traffic(f"c3batch_int8_gemv_11008x4096_m{M}")},
             "bytes_per_launch": bytes_,
             "timing": "graph replay of 64 launches rotating over 8 weight copies (> MALL)",
         })
@@ -294,7 +295,7 @@ def bench_c5_decode(steps, warmup):
             "metric": f"W8A16 FFN 4096-11008-4096 GB/s (M={M})",
             "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": _traffic(f"c5decode_ffn_w8a16_m{M}")},
             "bytes_per_launch": bytes_,
             "timing": "graph replay of 48 FFN calls (two GEMV launches each) rotating over "
                       "3 weight sets (> MALL)",
